@@ -1,0 +1,460 @@
+// C ABI of libgev2.so: descriptor validation, kernel selection and launch.
+// The kernels themselves live in gemm_tile_*.hip, gemm_skinny.hip and
+// gemm_aux.hip.  Nothing here throws across the ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/gev2_gemm.h"
+#include "gev2_kernels.hpp"
+
+namespace gev2 {
+int skinny_slab_cols(int dtype);
+int skinny_max_ks();
+
+hipError_t launch_tile(int dtype, int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
+                       int batch, hipStream_t s) {
+  switch (dtype) {
+    case GEV2_F32: return launch_tile_f32(cfg, ta, tb, pro, vec, a, batch, s);
+    case GEV2_BF16: return launch_tile_bf16(cfg, ta, tb, pro, vec, a, batch, s);
+    case GEV2_F16: return launch_tile_f16(cfg, ta, tb, pro, vec, a, batch, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+}  // namespace gev2
+
+namespace {
+
+thread_local std::string t_last_error;
+thread_local const char* t_last_path = "";
+
+int fail(int status, const std::string& msg) {
+  t_last_error = msg;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  t_last_error = std::string(where) + ": " + hipGetErrorString(e);
+  return GEV2_HIP_ERROR;
+}
+
+size_t elem_size(int dtype) { return dtype == GEV2_F32 ? 4 : 2; }
+int elems_per_chunk(int dtype) { return dtype == GEV2_F32 ? 4 : 8; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Vector (16-byte) loads of an operand are legal when its base is 16-byte
+// aligned and every row start and every chunk start is too.
+bool vec_ok(const void* p, int64_t ld, int64_t stride, int64_t contig_extent, int batch, int dtype) {
+  if (!p) return true;
+  const int epc = elems_per_chunk(dtype);
+  if (!aligned16(p) || ld % epc != 0 || contig_extent % epc != 0) return false;
+  if (batch > 1 && stride % epc != 0) return false;
+  return true;
+}
+
+bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffffLL; }
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  return std::atoi(v);
+}
+
+// Tile configuration heuristic: largest tile that still gives the 256 CUs at
+// least one workgroup each; GEV2_TILE_CFG overrides (tuning runs).
+int pick_cfg(int dtype, int64_t M, int64_t N, int64_t batch) {
+  const int forced = env_int("GEV2_TILE_CFG", -1);
+  if (forced >= 0) return forced;
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+  if (dtype != GEV2_F32) {
+    if (tiles(128, 256) >= 256) return gev2::kCfg128x256;
+    if (tiles(128, 128) >= 192) return gev2::kCfg128x128;
+    return gev2::kCfg64x64;
+  }
+  if (tiles(128, 128) >= 256) return gev2::kCfg128x128;
+  return gev2::kCfg64x64;
+}
+
+const char* cfg_name(int cfg, bool vec) {
+  if (!vec) return "tile:64x64:scalar";
+  switch (cfg) {
+    case gev2::kCfg256x256: return "tile:256x256";
+    case gev2::kCfg128x128: return "tile:128x128";
+    case gev2::kCfg64x64: return "tile:64x64";
+    case gev2::kCfg128x256: return "tile:128x256";
+    default: return "tile:?";
+  }
+}
+
+// Split-K workspace of the skinny kernel: one per (device, stream) so that
+// streams do not share partial sums.  Counters start at zero and every launch
+// leaves them at zero.
+struct SkinnyWs {
+  float* partial = nullptr;
+  size_t partial_bytes = 0;
+  unsigned* counters = nullptr;
+  size_t counter_count = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, SkinnyWs> g_ws;
+
+int get_skinny_ws(hipStream_t s, size_t partial_bytes, size_t counters, SkinnyWs** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  SkinnyWs& ws = g_ws[{dev, s}];
+  if (ws.partial_bytes < partial_bytes) {
+    if (ws.partial) (void)hipFree(ws.partial);
+    ws.partial = nullptr;
+    ws.partial_bytes = 0;
+    e = hipMalloc(&ws.partial, partial_bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(skinny partials)");
+    ws.partial_bytes = partial_bytes;
+  }
+  if (ws.counter_count < counters) {
+    // the previous counters may still be in use by queued work on this stream
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    if (ws.counters) (void)hipFree(ws.counters);
+    ws.counters = nullptr;
+    ws.counter_count = 0;
+    e = hipMalloc(&ws.counters, counters * sizeof(unsigned));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(skinny counters)");
+    e = hipMemset(ws.counters, 0, counters * sizeof(unsigned));
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(skinny counters)");
+    ws.counter_count = counters;
+  }
+  *out = &ws;
+  return GEV2_OK;
+}
+
+int check_common(int dtype, int act, int bias_kind, int64_t M, int64_t N, int64_t K, int64_t batch) {
+  if (dtype != GEV2_F32 && dtype != GEV2_F16 && dtype != GEV2_BF16)
+    return fail(GEV2_DTYPE_MISMATCH, "dtype must be F32, F16 or BF16");
+  if (act < GEV2_ACT_NONE || act > GEV2_ACT_TANH) return fail(GEV2_INVALID_ARGUMENT, "bad act kind");
+  if (bias_kind < GEV2_BIAS_NONE || bias_kind > GEV2_BIAS_PER_N)
+    return fail(GEV2_INVALID_ARGUMENT, "bad bias kind");
+  if (M < 0 || N < 0 || K < 0 || batch < 1) return fail(GEV2_SHAPE_MISMATCH, "negative dims or batch < 1");
+  if (!fits_i32(M) || !fits_i32(N) || !fits_i32(K) || !fits_i32(batch))
+    return fail(GEV2_INVALID, "dims must fit int32");
+  return GEV2_OK;
+}
+
+int64_t dense_ld(int64_t ld, int64_t cols) { return ld == 0 ? cols : ld; }
+
+}  // namespace
+
+extern "C" {
+
+int gev2_abi_version(void) { return GEV2_ABI_VERSION; }
+
+const char* gev2_last_error(void) { return t_last_error.c_str(); }
+const char* gev2_last_path(void) { return t_last_path; }
+
+const char* gev2_status_string(int s) {
+  switch (s) {
+    case GEV2_OK: return "Ok";
+    case GEV2_INVALID: return "Invalid";
+    case GEV2_UNIMPLEMENTED: return "Unimplemented";
+    case GEV2_RUNTIME_ERROR: return "RuntimeError";
+    case GEV2_INVALID_ARGUMENT: return "InvalidArgument";
+    case GEV2_MISSING_INPUT: return "MissingInput";
+    case GEV2_MISSING_OUTPUT: return "MissingOutput";
+    case GEV2_DEVICE_MISMATCH: return "DeviceMismatch";
+    case GEV2_DTYPE_MISMATCH: return "DtypeMismatch";
+    case GEV2_LAYOUT_MISMATCH: return "LayoutMismatch";
+    case GEV2_SHAPE_MISMATCH: return "ShapeMismatch";
+    case GEV2_STRIDE_MISMATCH: return "StrideMismatch";
+    case GEV2_TRANSPOSE_NOT_SUPPORTED: return "TransposeNotSupported";
+    case GEV2_HIP_ERROR: return "HipError";
+    default: return "Unknown";
+  }
+}
+
+int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
+  t_last_error.clear();
+  if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
+  int st = check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch);
+  if (st != GEV2_OK) return st;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  const int batch = static_cast<int>(d->batch);
+  if (!d->Y) return fail(GEV2_MISSING_OUTPUT, "Y is null");
+  if (K > 0 && (!d->A || !d->B)) return fail(GEV2_MISSING_INPUT, "A/B is null");
+  if (M == 0 || N == 0) return GEV2_OK;
+  const bool ta = d->trans_a != 0, tb = d->trans_b != 0;
+  const int64_t lda = dense_ld(d->lda, ta ? M : K), ldb = dense_ld(d->ldb, tb ? K : N);
+  const int64_t ldy = dense_ld(d->ldy, N), ldz = dense_ld(d->ldz, N);
+  if (lda < (ta ? M : K) || ldb < (tb ? K : N) || ldy < N || (d->Z && ldz < N))
+    return fail(GEV2_STRIDE_MISMATCH, "leading dimension smaller than the row length");
+  const bool has_bias = d->bias && d->bias_kind != GEV2_BIAS_NONE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  // ---- skinny path ----
+  const int epc = elems_per_chunk(d->dtype);
+  const bool skinny_ok = batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 &&
+                         N % epc == 0 && vec_ok(d->B, ldb, 0, N, 1, d->dtype) &&
+                         env_int("GEV2_NO_SKINNY", 0) == 0;
+  if (skinny_ok) {
+    const int slab = gev2::skinny_slab_cols(d->dtype);
+    const int64_t slabs = (N + slab - 1) / slab;
+    // splits: enough workgroups for 2 per CU, each split a multiple of the
+    // kernel's 128-row loop step
+    int64_t splits = std::max<int64_t>(1, (512 + slabs - 1) / slabs);
+    int64_t kps = (K + splits - 1) / splits;
+    kps = ((kps + 127) / 128) * 128;
+    if (kps > gev2::skinny_max_ks()) kps = gev2::skinny_max_ks();
+    splits = (K + kps - 1) / kps;
+    SkinnyWs* ws = nullptr;
+    st = get_skinny_ws(s, static_cast<size_t>(splits * M * N) * sizeof(float),
+                       static_cast<size_t>(slabs), &ws);
+    if (st != GEV2_OK) return st;
+    gev2::SkinnyArgs a{};
+    a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z;
+    a.bias = has_bias ? d->bias : nullptr;
+    a.partial = ws->partial; a.counters = ws->counters;
+    a.lda = lda; a.ldb = ldb; a.ldd = ldy; a.ldzo = ldz;
+    a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
+    a.act = d->act; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
+    a.slope = d->leaky_slope; a.alpha = d->alpha;
+    a.k_per_split = static_cast<int>(kps); a.splits = static_cast<int>(splits);
+    hipError_t e = gev2::launch_skinny(d->dtype, a, slab, s);
+    if (e != hipSuccess) return hip_fail(e, "skinny launch");
+    t_last_path = "skinny";
+    return GEV2_OK;
+  }
+
+  // ---- tile path ----
+  const bool vec = vec_ok(d->A, lda, d->stride_a, ta ? M : K, batch, d->dtype) &&
+                   vec_ok(d->B, ldb, d->stride_b, tb ? K : N, batch, d->dtype) &&
+                   env_int("GEV2_SCALAR_LOADS", 0) == 0;
+  const int cfg = pick_cfg(d->dtype, M, N, batch);
+  gev2::TileArgs a{};
+  a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z; a.Zi = nullptr;
+  a.bias = has_bias ? d->bias : nullptr; a.dbias = nullptr;
+  a.lda = lda; a.ldb = ldb; a.ldd = ldy; a.ldzo = ldz; a.ldzi = 0;
+  a.sA = d->stride_a; a.sB = d->stride_b; a.sD = d->stride_y; a.sZo = d->stride_z;
+  a.sZi = 0; a.sBias = d->stride_bias; a.sDbias = 0;
+  a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
+  a.act = d->act; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
+  a.slope = d->leaky_slope; a.alpha = d->alpha; a.pro_act = 0;
+  const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
+  a.tiles_m = static_cast<int>((M + bm - 1) / bm);
+  a.tiles_n = static_cast<int>((N + bn - 1) / bn);
+  a.store_vec = (aligned16(d->Y) && ldy % 4 == 0 && (batch == 1 || d->stride_y % 4 == 0) &&
+                 (!d->Z || (aligned16(d->Z) && ldz % 4 == 0 && (batch == 1 || d->stride_z % 4 == 0))))
+                    ? 1 : 0;
+  if (static_cast<int64_t>(a.tiles_m) * a.tiles_n > 0x7fffffffLL || batch > 65535)
+    return fail(GEV2_INVALID, "grid too large");
+  hipError_t e = gev2::launch_tile(d->dtype, cfg, ta, tb, 0, vec, a, batch, s);
+  if (e != hipSuccess) return hip_fail(e, "tile launch");
+  t_last_path = cfg_name(cfg, vec);
+  return GEV2_OK;
+}
+
+int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
+  t_last_error.clear();
+  if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
+  int st = check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch);
+  if (st != GEV2_OK) return st;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  const int batch = static_cast<int>(d->batch);
+  if (!d->gY || !d->Z) return fail(GEV2_MISSING_INPUT, "gY/Z is null");
+  if (d->gA && !d->B) return fail(GEV2_MISSING_INPUT, "gA requested but B is null");
+  if (d->gB && !d->A) return fail(GEV2_MISSING_INPUT, "gB requested but A is null");
+  const int64_t lda = dense_ld(d->lda, K), ldb = dense_ld(d->ldb, N);
+  const int64_t ldgy = dense_ld(d->ldgy, N), ldz = dense_ld(d->ldz, N);
+  const int64_t ldga = dense_ld(d->ldga, K), ldgb = dense_ld(d->ldgb, N), ldgc = dense_ld(d->ldgc, N);
+  if (lda < K || ldb < N || ldgy < N || ldz < N || ldga < K || ldgb < N || ldgc < N)
+    return fail(GEV2_STRIDE_MISMATCH, "leading dimension smaller than the row length");
+  if (M == 0 || N == 0 || K == 0) {
+    // the reference rejects empty problems in its backward (regemm_backward.cu:160)
+    return fail(GEV2_INVALID_ARGUMENT, "invalid dims");
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int dt = d->dtype;
+  const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
+  const bool fuse_bias = want_bias && d->bias_kind == GEV2_BIAS_PER_N && d->gB != nullptr;
+  const bool gyz_vec = vec_ok(d->gY, ldgy, d->stride_gy, N, batch, dt) &&
+                       vec_ok(d->Z, ldz, d->stride_z, N, batch, dt) &&
+                       env_int("GEV2_SCALAR_LOADS", 0) == 0;
+
+  // gA[M,K] = alpha * (gY (.) act'(Z)) [M,N] * B^T : NT, prologue on A
+  if (d->gA) {
+    const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, batch, dt);
+    const int cfg = pick_cfg(dt, M, K, batch);
+    gev2::TileArgs a{};
+    a.A = d->gY; a.lda = ldgy; a.sA = d->stride_gy;
+    a.Zi = d->Z; a.ldzi = ldz; a.sZi = d->stride_z;
+    a.B = d->B; a.ldb = ldb; a.sB = d->stride_b;
+    a.D = d->gA; a.ldd = ldga; a.sD = d->stride_ga;
+    a.M = static_cast<int>(M); a.N = static_cast<int>(K); a.K = static_cast<int>(N);
+    a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = d->alpha;
+    a.slope = d->leaky_slope; a.pro_act = d->act;
+    const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
+    a.tiles_m = static_cast<int>((M + bm - 1) / bm);
+    a.tiles_n = static_cast<int>((K + bn - 1) / bn);
+    a.store_vec = (aligned16(d->gA) && ldga % 4 == 0 && (batch == 1 || d->stride_ga % 4 == 0)) ? 1 : 0;
+    hipError_t e = gev2::launch_tile(dt, cfg, false, true, 1, vec, a, batch, s);
+    if (e != hipSuccess) return hip_fail(e, "dX launch");
+  }
+  // gB[K,N] = alpha * A^T [K,M] * (gY (.) act'(Z)) [M,N] : TN, prologue on B (+ dBias)
+  if (d->gB) {
+    const bool vec = gyz_vec && vec_ok(d->A, lda, d->stride_a, K, batch, dt);
+    const int cfg = pick_cfg(dt, K, N, batch);
+    gev2::TileArgs a{};
+    a.A = d->A; a.lda = lda; a.sA = d->stride_a;
+    a.B = d->gY; a.ldb = ldgy; a.sB = d->stride_gy;
+    a.Zi = d->Z; a.ldzi = ldz; a.sZi = d->stride_z;
+    a.D = d->gB; a.ldd = ldgb; a.sD = d->stride_gb;
+    a.dbias = fuse_bias ? d->gBias : nullptr; a.sDbias = d->stride_gbias;
+    a.M = static_cast<int>(K); a.N = static_cast<int>(N); a.K = static_cast<int>(M);
+    a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = d->alpha;
+    a.slope = d->leaky_slope; a.pro_act = d->act;
+    const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
+    a.tiles_m = static_cast<int>((K + bm - 1) / bm);
+    a.tiles_n = static_cast<int>((N + bn - 1) / bn);
+    a.store_vec = (aligned16(d->gB) && ldgb % 4 == 0 && (batch == 1 || d->stride_gb % 4 == 0)) ? 1 : 0;
+    hipError_t e = gev2::launch_tile(dt, cfg, true, false, 2, vec, a, batch, s);
+    if (e != hipSuccess) return hip_fail(e, "dW launch");
+  }
+  if (d->gC || (want_bias && !fuse_bias)) {
+    gev2::GradArgs g{};
+    g.gY = d->gY; g.Z = d->Z; g.out = d->gC; g.gbias = d->gBias;
+    g.ldgy = ldgy; g.ldz = ldz; g.ldout = ldgc;
+    g.sgY = d->stride_gy; g.sZ = d->stride_z; g.sOut = d->stride_gc; g.sGbias = d->stride_gbias;
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N);
+    g.act = d->act; g.slope = d->leaky_slope; g.beta = d->beta; g.bias_kind = d->bias_kind;
+    if (d->gC) {
+      hipError_t e = gev2::launch_grad_elementwise(dt, g, batch, s);
+      if (e != hipSuccess) return hip_fail(e, "gC launch");
+    }
+    if (want_bias && !fuse_bias) {
+      hipError_t e = gev2::launch_bias_grad(dt, g, batch, s);
+      if (e != hipSuccess) return hip_fail(e, "bias-grad launch");
+    }
+  }
+  return GEV2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Runtime helpers
+// ---------------------------------------------------------------------------
+#define GEV2_HIP_CALL(expr, where)                   \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return hip_fail(e_, where); \
+  } while (0)
+
+int gev2_device_count(int* count) {
+  GEV2_HIP_CALL(hipGetDeviceCount(count), "hipGetDeviceCount");
+  return GEV2_OK;
+}
+int gev2_set_device(int device) {
+  GEV2_HIP_CALL(hipSetDevice(device), "hipSetDevice");
+  return GEV2_OK;
+}
+int gev2_get_device(int* device) {
+  GEV2_HIP_CALL(hipGetDevice(device), "hipGetDevice");
+  return GEV2_OK;
+}
+int gev2_device_info(int device, char* name, size_t name_len, int* cu_count, int* clock_khz) {
+  hipDeviceProp_t prop;
+  GEV2_HIP_CALL(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (name && name_len) {
+    std::snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  return GEV2_OK;
+}
+int gev2_malloc(void** ptr, size_t bytes) {
+  GEV2_HIP_CALL(hipMalloc(ptr, bytes), "hipMalloc");
+  return GEV2_OK;
+}
+int gev2_free(void* ptr) {
+  GEV2_HIP_CALL(hipFree(ptr), "hipFree");
+  return GEV2_OK;
+}
+int gev2_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  GEV2_HIP_CALL(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  return GEV2_OK;
+}
+int gev2_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  GEV2_HIP_CALL(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  return GEV2_OK;
+}
+int gev2_memcpy_dtod_async(void* dst, const void* src, size_t bytes, void* stream) {
+  GEV2_HIP_CALL(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                               reinterpret_cast<hipStream_t>(stream)),
+                "hipMemcpyAsync D2D");
+  return GEV2_OK;
+}
+int gev2_memset(void* ptr, int value, size_t bytes) {
+  GEV2_HIP_CALL(hipMemset(ptr, value, bytes), "hipMemset");
+  return GEV2_OK;
+}
+int gev2_stream_create(void** stream) {
+  hipStream_t s;
+  GEV2_HIP_CALL(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = s;
+  return GEV2_OK;
+}
+int gev2_stream_destroy(void* stream) {
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (auto it = g_ws.begin(); it != g_ws.end();) {
+      if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
+        (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+        if (it->second.partial) (void)hipFree(it->second.partial);
+        if (it->second.counters) (void)hipFree(it->second.counters);
+        it = g_ws.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+  GEV2_HIP_CALL(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  return GEV2_OK;
+}
+int gev2_stream_synchronize(void* stream) {
+  GEV2_HIP_CALL(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+  return GEV2_OK;
+}
+int gev2_device_synchronize(void) {
+  GEV2_HIP_CALL(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return GEV2_OK;
+}
+int gev2_event_create(void** event) {
+  hipEvent_t e;
+  GEV2_HIP_CALL(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return GEV2_OK;
+}
+int gev2_event_destroy(void* event) {
+  GEV2_HIP_CALL(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy");
+  return GEV2_OK;
+}
+int gev2_event_record(void* event, void* stream) {
+  GEV2_HIP_CALL(hipEventRecord(reinterpret_cast<hipEvent_t>(event), reinterpret_cast<hipStream_t>(stream)),
+                "hipEventRecord");
+  return GEV2_OK;
+}
+int gev2_event_synchronize(void* event) {
+  GEV2_HIP_CALL(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
+  return GEV2_OK;
+}
+int gev2_event_elapsed_ms(float* ms, void* start, void* stop) {
+  GEV2_HIP_CALL(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)),
+                "hipEventElapsedTime");
+  return GEV2_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,141 @@
+// Small backward helpers for the cases the fused MFMA passes do not cover:
+//   - gC = beta * gY (.) act'(Z)          (regemm_backward.cu:116-118)
+//   - bias gradient when it cannot ride the dW pass: PerM (row sums), Scalar,
+//     or PerN without a dW output.  (regemm_backward.cu:120-129 accumulates
+//     these with fp32 atomics; here every sum has a fixed order.)
+#include "gev2_device.hpp"
+#include "gev2_kernels.hpp"
+
+namespace gev2 {
+
+template <typename T>
+__global__ void __launch_bounds__(256) grad_elementwise_kernel(GradArgs p) {
+  const int bz = blockIdx.y;
+  const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
+  const T* Z = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ;
+  T* out = reinterpret_cast<T*>(p.out) + (int64_t)bz * p.sOut;
+  const int64_t total = (int64_t)p.M * p.N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int m = static_cast<int>(i / p.N), n = static_cast<int>(i - (int64_t)m * p.N);
+    const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
+    const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
+    Elem<T>::store1(out + (int64_t)m * p.ldout + n, p.beta * (g * act_grad(z, p.act, p.slope)));
+  }
+}
+
+// PerN: 64 columns x 4 row lanes per workgroup; each thread walks its rows in
+// order, then the 4 lanes are added in order.
+template <typename T>
+__global__ void __launch_bounds__(256) bias_grad_cols_kernel(GradArgs p) {
+  __shared__ float red[4][64];
+  const int bz = blockIdx.y;
+  const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
+  const T* Z = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ;
+  const int c = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + c;
+  float s = 0.f;
+  if (n < p.N) {
+    for (int m = r; m < p.M; m += 4) {
+      const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
+      const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
+      s += g * act_grad(z, p.act, p.slope);
+    }
+  }
+  red[r][c] = s;
+  __syncthreads();
+  if (r == 0 && n < p.N) p.gbias[(int64_t)bz * p.sGbias + n] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// PerM: one wave per row.
+template <typename T>
+__global__ void __launch_bounds__(256) bias_grad_rows_kernel(GradArgs p) {
+  const int bz = blockIdx.y;
+  const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
+  const T* Z = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ;
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= p.M) return;
+  float s = 0.f;
+  for (int n = lane; n < p.N; n += 64) {
+    const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
+    const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
+    s += g * act_grad(z, p.act, p.slope);
+  }
+  s = wave_sum(s);
+  if (lane == 0) p.gbias[(int64_t)bz * p.sGbias + m] = s;
+}
+
+// Scalar: one workgroup per slice sums everything.
+template <typename T>
+__global__ void __launch_bounds__(256) bias_grad_all_kernel(GradArgs p) {
+  __shared__ float red[4];
+  const int bz = blockIdx.y;
+  const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
+  const T* Z = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ;
+  const int64_t total = (int64_t)p.M * p.N;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < total; i += 256) {
+    const int m = static_cast<int>(i / p.N), n = static_cast<int>(i - (int64_t)m * p.N);
+    const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
+    const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
+    s += g * act_grad(z, p.act, p.slope);
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) p.gbias[(int64_t)bz * p.sGbias] = red[0] + red[1] + red[2] + red[3];
+}
+
+template <typename T>
+static hipError_t grad_elementwise_t(const GradArgs& a, int batch, hipStream_t s) {
+  const int64_t total = (int64_t)a.M * a.N;
+  int64_t nb = (total + 255) / 256;
+  int blocks = static_cast<int>(nb < 4096 ? nb : 4096);
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(grad_elementwise_kernel<T>, dim3(blocks, batch), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t bias_grad_t(const GradArgs& a, int batch, hipStream_t s) {
+  switch (a.bias_kind) {
+    case kBiasPerN:
+      hipLaunchKernelGGL(bias_grad_cols_kernel<T>, dim3((a.N + 63) / 64, batch), dim3(256), 0, s, a);
+      break;
+    case kBiasPerM:
+      hipLaunchKernelGGL(bias_grad_rows_kernel<T>, dim3((a.M + 3) / 4, batch), dim3(256), 0, s, a);
+      break;
+    case kBiasScalar:
+      hipLaunchKernelGGL(bias_grad_all_kernel<T>, dim3(1, batch), dim3(256), 0, s, a);
+      break;
+    default: return hipSuccess;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s) {
+  switch (dtype) {
+    case kF32: return grad_elementwise_t<float>(a, batch, s);
+    case kBF16: return grad_elementwise_t<__bf16>(a, batch, s);
+    case kF16: return grad_elementwise_t<_Float16>(a, batch, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_bias_grad(int dtype, const GradArgs& a, int batch, hipStream_t s) {
+  switch (dtype) {
+    case kF32: return bias_grad_t<float>(a, batch, s);
+    case kBF16: return bias_grad_t<__bf16>(a, batch, s);
+    case kF16: return bias_grad_t<_Float16>(a, batch, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace gev2

@@ -1,0 +1,10 @@
+// Instantiations of the MFMA tile GEMM for one element type (_Float16); split per
+// type so the three compile in parallel.
+#include "gemm_tile_impl.hpp"
+
+namespace gev2 {
+hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
+                          int batch, hipStream_t s) {
+  return launch_cfg<_Float16>(cfg, ta, tb, pro, vec, a, batch, s);
+}
+}  // namespace gev2

@@ -1,0 +1,91 @@
+// Kernel argument blocks and launcher declarations shared between the HIP
+// kernels (gemm_tile.hip, gemm_skinny.hip, gemm_aux.hip) and the C-ABI
+// dispatcher (capi.hip).  All strides and leading dimensions are in elements.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gev2 {
+
+// One launch of the MFMA tile kernel computes, for each batch slice b,
+//   D = epilogue( alpha * op(A) @ op(B) )
+// where op(A) is [M,K] and op(B) is [K,N].  Operand layouts:
+//   trans_a = 0: A is [M,K] row-major (lda >= K);  1: A is [K,M] (lda >= M)
+//   trans_b = 0: B is [K,N] row-major (ldb >= N);  1: B is [N,K] (ldb >= K)
+// A "prologue" may replace one operand element-wise by  g * act'(z)  with z
+// read from Zi at the same logical position (the backward pass's dY' = dY (.)
+// act'(Z)), and, for the [K,N] operand, also emit its column sums (dBias).
+struct TileArgs {
+  const void* A; const void* B; void* D; void* Zo;
+  const void* Zi;        // prologue pre-activation (same layout as the operand it scales)
+  const float* bias;     // epilogue bias (kind below)
+  float* dbias;          // fused column sums of the prologue operand (PerN dBias)
+  int64_t lda, ldb, ldd, ldzo, ldzi;
+  int64_t sA, sB, sD, sZo, sZi, sBias, sDbias;   // batch strides
+  int M, N, K;
+  int act, bias_kind;    // epilogue
+  float slope, alpha;
+  int pro_act;           // prologue activation kind (derivative applied)
+  int tiles_m, tiles_n;
+  int store_vec;         // D/Zo rows allow 4-wide vector stores
+};
+
+// Skinny forward (M <= kSkinnyMaxM): split-K streaming over B with a
+// deterministic last-workgroup reduction of the fp32 partials.
+constexpr int kSkinnyMaxM = 16;
+struct SkinnyArgs {
+  const void* A; const void* B; void* D; void* Zo;
+  const float* bias;
+  float* partial;        // [splits][M][N] fp32 workspace
+  unsigned* counters;    // [n_slabs] arrival counters, zero between launches
+  int64_t lda, ldb, ldd, ldzo;
+  int M, N, K;
+  int act, bias_kind;
+  float slope, alpha;
+  int k_per_split, splits;
+};
+
+// Element-wise gZ = gY * act'(Z) (optionally scaled by beta) -> out, and
+// deterministic bias-gradient reductions.
+struct GradArgs {
+  const void* gY; const void* Z; void* out;      // out may be null
+  float* gbias;                                   // may be null
+  int64_t ldgy, ldz, ldout;
+  int64_t sgY, sZ, sOut, sGbias;
+  int M, N;
+  int act; float slope; float beta;
+  int bias_kind;
+};
+
+// Launcher entry points (each returns hipError_t from the launch).
+// Tile configuration ids, chosen by the host dispatcher.
+enum TileCfg : int {
+  kCfg256x256 = 0,   // 16-bit: 256x256x64 tile, 8 waves (128x64 per wave)
+  kCfg128x128 = 1,   // 128x128, 4 waves (64x64 per wave)
+  kCfg64x64 = 2,     // 64x64, 4 waves (32x32 per wave)
+  kCfg128x256 = 3,   // 128x256, 4 waves (64x128 per wave)
+};
+
+hipError_t launch_tile(int dtype, int cfg, bool trans_a, bool trans_b, int prologue,
+                       bool vec, const TileArgs& a, int batch, hipStream_t s);
+hipError_t launch_tile_f32(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
+                           int batch, hipStream_t s);
+hipError_t launch_tile_bf16(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
+                            int batch, hipStream_t s);
+hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
+                           int batch, hipStream_t s);
+hipError_t launch_skinny(int dtype, const SkinnyArgs& a, int slab_cols, hipStream_t s);
+hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s);
+hipError_t launch_bias_grad(int dtype, const GradArgs& a, int batch, hipStream_t s);
+
+// Tile extents of each configuration (scalar-load variants always use 64x64).
+inline int tile_bm(int cfg, bool vec) {
+  if (!vec) return 64;
+  return cfg == kCfg256x256 ? 256 : cfg == kCfg64x64 ? 64 : 128;
+}
+inline int tile_bn(int cfg, bool vec) {
+  if (!vec) return 64;
+  return cfg == kCfg256x256 ? 256 : cfg == kCfg64x64 ? 64 : cfg == kCfg128x256 ? 256 : 128;
+}
+
+}  // namespace gev2

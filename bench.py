@@ -1,0 +1,375 @@
+#!/usr/bin/env python3
+"""Benchmark of the GEMM + bias + activation operator on one MI355X.
+
+Headline: bf16 X[4096,4096] W[4096,4096] + bias,
+ReLU, Z stash; one *step* = forward + backward (gA, gB, gBias), inputs resident
+in HBM.  value = 6*M*N*K / step time (TFLOP/s).
+
+roofline: the forward GEMM+bias+ReLU kernel timed alone with HIP events on the
+stream it is launched on; achieved = 2*M*N*K / average launch time, against the
+dense bf16 MFMA peak (2516.6 TFLOP/s).
+
+cpu_baseline: the reference's NumPy path (smoke_gemm_binding.py:84-123,
+restated in oracle/gemm_oracle.py) in fp32 on the host's cores, on a bounded
+row-slice of the same workload.
+
+Extra fields time the other BASELINE configs (C1, C2, C3-fp16, C4 SDPA batched,
+C5a conv-as-GEMM, C5b skinny); the bandwidth-bound ones rotate buffer sets
+totalling > 256 MB so that reads come from HBM, not the MALL.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "ai_framework-dev_amd"))
+
+PEAK_BF16 = 2516.6   # dense bf16/fp16 MFMA TFLOP/s (MI355X)
+PEAK_F32 = 157.3     # fp32 MFMA TFLOP/s
+PEAK_HBM = 8000.0    # GB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of extra configs to run")
+    return ap.parse_args()
+
+
+class Ctx:
+    def __init__(self, capi):
+        self.capi = capi
+        self.stream = capi.Stream()
+        self.bufs = []
+
+    def put(self, a):
+        b = self.capi.DeviceBuffer.from_numpy(a)
+        self.bufs.append(b)
+        return b.ptr
+
+    def empty(self, nbytes):
+        b = self.capi.DeviceBuffer(nbytes)
+        self.bufs.append(b)
+        return b.ptr
+
+    def free(self):
+        for b in self.bufs:
+            b.free()
+        self.bufs = []
+
+    def time_ms(self, fn, iters, warmup=3):
+        """Average ms per call of fn() (which launches on self.stream)."""
+        capi = self.capi
+        for _ in range(warmup):
+            fn()
+        self.stream.synchronize()
+        e0, e1 = capi.Event(), capi.Event()
+        e0.record(self.stream.ptr)
+        for _ in range(iters):
+            fn()
+        e1.record(self.stream.ptr)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / iters
+        e0.destroy()
+        e1.destroy()
+        return ms
+
+
+def normal(g, shape, scale=1.0):
+    return (g.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+
+
+# ---------------------------------------------------------------------------
+def headline(ctx, steps, warmup, dtype, M=4096, N=4096, K=4096, seed=3):
+    capi = ctx.capi
+    g = np.random.default_rng(seed)
+    X = capi.to_storage(normal(g, (M, K), 1 / np.sqrt(K)), dtype)
+    W = capi.to_storage(normal(g, (K, N), 1 / np.sqrt(K)), dtype)
+    b = normal(g, (N,), 0.02)
+    gY = capi.to_storage(normal(g, (M, N)), dtype)
+    es = capi.elem_bytes(dtype)
+    pX, pW, pb, pgY = ctx.put(X), ctx.put(W), ctx.put(b), ctx.put(gY)
+    pY, pZ = ctx.empty(M * N * es), ctx.empty(M * N * es)
+    pgA, pgB, pgb = ctx.empty(M * K * es), ctx.empty(K * N * es), ctx.empty(N * 4)
+    s = ctx.stream.ptr
+
+    def fwd():
+        capi.gemm_fwd(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
+                      bias_kind=capi.BIAS_PERN, act="relu", stream=s)
+
+    def bwd():
+        capi.gemm_bwd(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
+                      gBias=pgb, bias_kind=capi.BIAS_PERN, act="relu", stream=s)
+
+    def step():
+        fwd()
+        bwd()
+
+    fwd()
+    path = capi.last_path()
+    # timed region: exactly `steps` steps, synchronised on both sides
+    for _ in range(warmup):
+        step()
+    ctx.stream.synchronize()
+    e0, e1 = capi.Event(), capi.Event()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(steps):
+        step()
+    e1.record(s)
+    e1.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = e0.elapsed_ms(e1) / steps
+    fwd_ms = ctx.time_ms(fwd, max(steps, 20))
+    bwd_ms = ctx.time_ms(bwd, max(steps, 20))
+    flop = 2.0 * M * N * K
+    return {
+        "step_ms": step_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "wall_s": wall, "path": path,
+        "tflops_step": 3 * flop / (step_ms * 1e-3) / 1e12,
+        "tflops_fwd": flop / (fwd_ms * 1e-3) / 1e12,
+        "tflops_bwd": 2 * flop / (bwd_ms * 1e-3) / 1e12,
+        "fwd_bytes": (M * K + K * N + 2 * M * N) * es + N * 4,
+    }
+
+
+def fp32_cfg(ctx, M, N, K, act, iters, seed):
+    """C1 / C2: fp32 GEMM + bias + act, forward and forward+backward."""
+    capi = ctx.capi
+    g = np.random.default_rng(seed)
+    if M == 64:
+        X = g.uniform(-1, 1, (M, K)).astype(np.float32) / np.float32(np.sqrt(K))
+        W = g.uniform(-1, 1, (K, N)).astype(np.float32) / np.float32(np.sqrt(K))
+        b = g.uniform(-1, 1, (N,)).astype(np.float32) / np.float32(np.sqrt(K))
+    else:
+        X, W, b = normal(g, (M, K), 1 / np.sqrt(K)), normal(g, (K, N), 1 / np.sqrt(K)), normal(g, (N,), 0.02)
+    gY = normal(g, (M, N))
+    pX, pW, pb, pgY = ctx.put(X), ctx.put(W), ctx.put(b), ctx.put(gY)
+    pY, pZ = ctx.empty(M * N * 4), ctx.empty(M * N * 4)
+    pgA, pgB, pgb = ctx.empty(M * K * 4), ctx.empty(K * N * 4), ctx.empty(N * 4)
+    s = ctx.stream.ptr
+
+    def fwd():
+        capi.gemm_fwd(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
+                      bias_kind=capi.BIAS_PERN, act=act, stream=s)
+
+    def step():
+        fwd()
+        capi.gemm_bwd(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
+                      gBias=pgb, bias_kind=capi.BIAS_PERN, act=act, stream=s)
+
+    fwd_ms = ctx.time_ms(fwd, iters)
+    step_ms = ctx.time_ms(step, iters)
+    flop = 2.0 * M * N * K
+    return {"fwd_us": fwd_ms * 1e3, "step_us": step_ms * 1e3,
+            "tflops_fwd": flop / (fwd_ms * 1e-3) / 1e12,
+            "tflops_step": 3 * flop / (step_ms * 1e-3) / 1e12,
+            "frac_fwd": flop / (fwd_ms * 1e-3) / 1e12 / PEAK_F32}
+
+
+def sdpa_cfg(ctx, dtype, iters, sets=8):
+    """C4: batched QK^T (scale 1/8, trans_b) and P.V, B*H = 64, 512x512x64."""
+    capi = ctx.capi
+    BH, L, D = 64, 512, 64
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(44)
+    bufs = []
+    for _ in range(sets):
+        Q = capi.to_storage(normal(g, (BH, L, D)), dtype)
+        Kt = capi.to_storage(normal(g, (BH, L, D)), dtype)
+        V = capi.to_storage(normal(g, (BH, L, D)), dtype)
+        logits = normal(g, (BH, L, L))
+        P = np.exp(logits - logits.max(-1, keepdims=True))
+        P /= P.sum(-1, keepdims=True)
+        bufs.append((ctx.put(Q), ctx.put(Kt), ctx.put(V), ctx.put(capi.to_storage(P, dtype)),
+                     ctx.empty(BH * L * L * es), ctx.empty(BH * L * D * es)))
+    s = ctx.stream.ptr
+    it = [0]
+
+    def qk():
+        q, k, _, _, S, _ = bufs[it[0] % sets]
+        it[0] += 1
+        capi.gemm_fwd(dtype=dtype, M=L, N=L, K=D, A=q, B=k, Y=S, trans_b=True, alpha=0.125,
+                      batch=BH, stride_a=L * D, stride_b=L * D, stride_y=L * L, stream=s)
+
+    def pv():
+        _, _, v, p, _, y = bufs[it[0] % sets]
+        it[0] += 1
+        capi.gemm_fwd(dtype=dtype, M=L, N=D, K=L, A=p, B=v, Y=y, batch=BH,
+                      stride_a=L * L, stride_b=L * D, stride_y=L * D, stream=s)
+
+    qk_ms = ctx.time_ms(qk, iters)
+    pv_ms = ctx.time_ms(pv, iters)
+    flop = 2.0 * BH * L * L * D
+    byt_qk = (2 * BH * L * D + BH * L * L) * es
+    byt_pv = (BH * L * L + 2 * BH * L * D) * es
+    return {"qk_us": qk_ms * 1e3, "pv_us": pv_ms * 1e3,
+            "qk_gbps": byt_qk / (qk_ms * 1e-3) / 1e9, "pv_gbps": byt_pv / (pv_ms * 1e-3) / 1e9,
+            "qk_frac_hbm": byt_qk / (qk_ms * 1e-3) / 1e9 / PEAK_HBM,
+            "pv_frac_hbm": byt_pv / (pv_ms * 1e-3) / 1e9 / PEAK_HBM,
+            "tflops_qk": flop / (qk_ms * 1e-3) / 1e12, "tflops_pv": flop / (pv_ms * 1e-3) / 1e12}
+
+
+def conv_cfg(ctx, dtype, iters):
+    """C5a: im2col-lowered conv2d as one GEMM, M=100352, K=576, N=128, bias + ReLU (Z saved)."""
+    capi = ctx.capi
+    M, K, N = 32 * 56 * 56, 64 * 9, 128
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(55)
+    col = capi.to_storage(g.random((M, K), dtype=np.float32), dtype)
+    W = capi.to_storage(normal(g, (K, N), np.sqrt(2 / 576)), dtype)
+    b = normal(g, (N,), 0.02)
+    pA, pW, pb = ctx.put(col), ctx.put(W), ctx.put(b)
+    pY, pZ = ctx.empty(M * N * es), ctx.empty(M * N * es)
+    s = ctx.stream.ptr
+
+    def fwd():
+        capi.gemm_fwd(dtype=dtype, M=M, N=N, K=K, A=pA, B=pW, Y=pY, Z=pZ, bias=pb,
+                      bias_kind=capi.BIAS_PERN, act="relu", stream=s)
+
+    ms = ctx.time_ms(fwd, iters)
+    flop = 2.0 * M * N * K
+    byt = (M * K + K * N + 2 * M * N) * es + N * 4
+    peak = PEAK_F32 if dtype == capi.F32 else PEAK_BF16
+    t_roof = max(flop / (peak * 1e12), byt / (PEAK_HBM * 1e9))
+    return {"fwd_us": ms * 1e3, "tflops": flop / (ms * 1e-3) / 1e12,
+            "gbps": byt / (ms * 1e-3) / 1e9, "roofline_frac": t_roof / (ms * 1e-3)}
+
+
+def skinny_cfg(ctx, iters, sets=10):
+    """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL."""
+    capi = ctx.capi
+    M, N, K = 8, 4096, 4096
+    g = np.random.default_rng(66)
+    X = capi.to_storage(normal(g, (M, K), 1 / np.sqrt(K)), capi.BF16)
+    pX = ctx.put(X)
+    pb = ctx.put(normal(g, (N,), 0.02))
+    Ws = [ctx.put(capi.to_storage(normal(g, (K, N), 1 / np.sqrt(K)), capi.BF16)) for _ in range(sets)]
+    pY = ctx.empty(M * N * 2)
+    s = ctx.stream.ptr
+    it = [0]
+
+    def fwd():
+        w = Ws[it[0] % sets]
+        it[0] += 1
+        capi.gemm_fwd(dtype=capi.BF16, M=M, N=N, K=K, A=pX, B=w, Y=pY, bias=pb,
+                      bias_kind=capi.BIAS_PERN, act="none", stream=s)
+
+    fwd()
+    path = capi.last_path()
+    ms = ctx.time_ms(fwd, iters)
+    byt = (M * K + K * N + M * N) * 2 + N * 4
+    return {"fwd_us": ms * 1e3, "gbps": byt / (ms * 1e-3) / 1e9,
+            "frac_hbm": byt / (ms * 1e-3) / 1e9 / PEAK_HBM, "path": path}
+
+
+def cpu_baseline(M=4096, N=4096, K=4096, rows=512, reps=3):
+    """fp32 NumPy forward+backward (the reference's CPU path) on a row slice."""
+    from oracle import gemm_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        blas = ",".join(sorted({i.get("internal_api", "?") for i in threadpool_info()}))
+    except Exception:
+        threads, blas = len(os.sched_getaffinity(0)), "?"
+    g = np.random.default_rng(7)
+    X = normal(g, (rows, K), 1 / np.sqrt(K))
+    W = normal(g, (K, N), 1 / np.sqrt(K))
+    b = normal(g, (1, N), 0.02)
+    gY = normal(g, (rows, N))
+    O.numpy_fp32_step(X, W, b, gY, "relu")   # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.numpy_fp32_step(X, W, b, gY, "relu")
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    flop = 6.0 * rows * N * K
+    return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"fp32 numpy fwd+bwd (np.matmul, {blas}) on a {rows}-row slice of the "
+                      f"4096^3 step ({rows}x{K} @ {K}x{N}), median of {reps}; "
+                      f"{t * 1e3:.1f} ms per slice, full step extrapolates to "
+                      f"{t * M / rows:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the operator's multi-GPU "
+                          "sharding is design-only (see DESIGN.md); run with --gpus 1"}))
+        return 2
+    from graph_executor_v2.ops import capi
+    capi.lib()
+    if capi.device_count() < 1:
+        raise SystemExit("no HIP device visible")
+    name, cus, clk = capi.device_info(0)
+    ctx = Ctx(capi)
+    res = headline(ctx, args.steps, args.warmup, capi.BF16)
+    print(f"# headline bf16 4096^3: step {res['step_ms']:.3f} ms, fwd {res['fwd_ms'] * 1e3:.1f} us "
+          f"({res['tflops_fwd']:.0f} TFLOP/s), bwd {res['bwd_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
+    ctx.free()
+    extra = {"device": name, "cus": cus, "peak_clock_mhz": clk / 1000.0,
+             "fwd_ms": res["fwd_ms"], "bwd_ms": res["bwd_ms"], "path": res["path"],
+             "tflops_fwd": res["tflops_fwd"], "tflops_bwd": res["tflops_bwd"]}
+    if not args.quick:
+        only = set(filter(None, args.only.split(",")))
+        todo = [
+            ("c1_mlp_f32_64x784x256_relu", lambda: fp32_cfg(ctx, 64, 256, 784, "relu", 200, 1)),
+            ("c2_f32_1024_gelu", lambda: fp32_cfg(ctx, 1024, 1024, 1024, "gelu", 50, 2)),
+            ("c3_f16_4096_relu", lambda: headline(ctx, 10, 3, capi.F16)),
+            ("c4_sdpa_bf16", lambda: sdpa_cfg(ctx, capi.BF16, 50)),
+            ("c5a_conv_f32", lambda: conv_cfg(ctx, capi.F32, 20)),
+            ("c5a_conv_bf16", lambda: conv_cfg(ctx, capi.BF16, 20)),
+            ("c5b_skinny_bf16", lambda: skinny_cfg(ctx, 100)),
+        ]
+        for key, fn in todo:
+            if only and key not in only:
+                continue
+            r = fn()
+            ctx.free()
+            if key == "c3_f16_4096_relu":
+                r = {k: r[k] for k in ("step_ms", "fwd_ms", "bwd_ms", "tflops_step", "tflops_fwd")}
+            extra[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+            print(f"# {key}: {extra[key]}", file=sys.stderr, flush=True)
+    flop = 2.0 * 4096 ** 3
+    achieved = flop / (res["fwd_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "GEMM+bias+act TFLOP/s and % MFMA peak at 4096^3 bf16; fwd+bwd step ms",
+        "value": round(res["tflops_step"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1/K) X and W, N(0,0.02) bias, N(0,1) dY)",
+        "config": {"workload": "C3: Y=ReLU(X W + b), X[4096,4096] W[4096,4096] bf16, fp32 accumulate, "
+                               "Z saved; step = forward + backward (dX, dW, dBias)",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
+                     "kernel": "gemm_tile_kernel (forward, bf16 " + res["path"] + ")",
+                     "flop_per_launch": flop},
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

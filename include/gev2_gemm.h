@@ -1,0 +1,165 @@
+/*
+ * gev2_gemm.h -- C ABI of the MI355X (gfx950) GEMM + bias + activation
+ * operator (libgev2.so).
+ *
+ * This is the thin C layer that the C++ host code behind the Python binding
+ * (graph_executor_v2.ops._ops_gemm) calls.  It replaces, one for one:
+ *   gev2_gemm_fwd  <- ai::cuda::shim::GemmCudaLaunch
+ *                     (graph_executor_v2/backends/cuda/ops/gemm/api.hpp:509-518,
+ *                      launcher.cu:147-274) and, with batch > 1 or a transpose,
+ *                     the per-slice GEMM loops of conv2d/launcher.cu:180-227 and
+ *                     sdpa/launcher.cu:185-270
+ *   gev2_gemm_bwd  <- ai::cuda::shim::GemmCudaBackward / GemmCudaBackwardInto
+ *                     (gemm/api.hpp:535-573, launcher.cu:279-383,
+ *                      kernels/regemm_backward.cu:151-301)
+ * Its descriptor style (one POD of pointers, sizes and enums per call) follows
+ * the reference's earlier C ABI, dev/backend/graph_executor_v2/include/
+ * ge_v2_api_ex.h:37-134.
+ *
+ * Conventions
+ *   - All matrices are row-major.  Leading dimensions (ld*) and batch strides
+ *     (stride_*) are in elements.  ld* == 0 means "dense" (number of columns).
+ *   - dtype applies to A, B, Y, Z, gY, gA, gB, gC; bias and gBias are float32.
+ *   - Return values are the reference's Status codes (enums.hpp / ai_status.hpp):
+ *     GEV2_HIP_ERROR (130) is the reference's CUDA_ERROR slot.  The functions
+ *     never throw; gev2_last_error() gives a message for the calling thread.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = null stream).
+ *   - gev2_gemm_fwd with 1 <= M <= 16 uses a split-K kernel whose partial sums
+ *     live in a workspace the library allocates once per (device, stream) on
+ *     first use: make that first call outside HIP-graph capture.
+ */
+#ifndef GEV2_GEMM_H_
+#define GEV2_GEMM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEV2_ABI_VERSION 1
+
+/* Status (values of ai::cuda::shim::Status, ai_status.hpp:14-43) */
+enum {
+  GEV2_OK = 0,
+  GEV2_INVALID = 1,
+  GEV2_UNIMPLEMENTED = 2,
+  GEV2_RUNTIME_ERROR = 3,
+  GEV2_INVALID_ARGUMENT = 4,
+  GEV2_MISSING_INPUT = 10,
+  GEV2_MISSING_OUTPUT = 11,
+  GEV2_DEVICE_MISMATCH = 100,
+  GEV2_DTYPE_MISMATCH = 101,
+  GEV2_LAYOUT_MISMATCH = 102,
+  GEV2_SHAPE_MISMATCH = 103,
+  GEV2_STRIDE_MISMATCH = 104,
+  GEV2_TRANSPOSE_NOT_SUPPORTED = 105,
+  GEV2_HIP_ERROR = 130,
+  GEV2_UNKNOWN = 999
+};
+
+/* DType (ai_device.hpp:14-27), ActKind and BiasKind (enums.hpp:10-24) */
+enum { GEV2_F32 = 0, GEV2_F16 = 1, GEV2_BF16 = 2 };
+enum { GEV2_ACT_NONE = 0, GEV2_ACT_RELU = 1, GEV2_ACT_LEAKY_RELU = 2, GEV2_ACT_GELU = 3,
+       GEV2_ACT_SIGMOID = 4, GEV2_ACT_TANH = 5 };
+enum { GEV2_BIAS_NONE = 0, GEV2_BIAS_SCALAR = 1, GEV2_BIAS_PER_M = 2, GEV2_BIAS_PER_N = 3 };
+
+/*
+ * Forward, for each slice b < batch:
+ *   Z_b = alpha * op(A_b) op(B_b) + bias_b          (op(A) is [M,K], op(B) is [K,N])
+ *   Y_b = act(Z_b)
+ * trans_a = 0: A is [M,K] (lda >= K);  1: A is stored [K,M] (lda >= M).
+ * trans_b = 0: B is [K,N] (ldb >= N);  1: B is stored [N,K] (ldb >= K).
+ * Z may be NULL (no pre-activation stash); Z == Y is allowed.
+ * bias may be NULL or bias_kind NONE; PerN indexes bias[n], PerM bias[m].
+ * Replaces GemmCudaLaunch (launcher.cu:147-274), which only has batch = 1,
+ * alpha = 1 and no transposes (it returns TransposeNotSupported for them).
+ */
+typedef struct gev2_gemm_fwd_desc {
+  int32_t dtype;
+  int32_t act;
+  int32_t bias_kind;
+  int32_t trans_a;
+  int32_t trans_b;
+  float leaky_slope;
+  float alpha;
+  int32_t reserved0;
+  int64_t M, N, K, batch;
+  const void* A;     int64_t lda, stride_a;
+  const void* B;     int64_t ldb, stride_b;
+  const float* bias; int64_t stride_bias;
+  void* Y;           int64_t ldy, stride_y;
+  void* Z;           int64_t ldz, stride_z;
+} gev2_gemm_fwd_desc;
+
+/*
+ * Backward of the forward above (trans_a = trans_b = 0), for each slice:
+ *   gZ = gY (.) act'(Z)                       (never written to memory)
+ *   gA = alpha * gZ B^T        [M,K]   (optional)
+ *   gB = alpha * A^T gZ        [K,N]   (optional)
+ *   gC = beta * gZ             [M,N]   (optional)
+ *   gBias = sum of gZ over rows (PER_N, [N]) / columns (PER_M, [M]) / all (SCALAR)
+ * Replaces GemmCudaBackward (launcher.cu:279-383 + regemm_backward.cu:151-301).
+ * gBias is overwritten (the reference zero-fills it first, :190-197).
+ */
+typedef struct gev2_gemm_bwd_desc {
+  int32_t dtype;
+  int32_t act;
+  int32_t bias_kind;
+  float leaky_slope;
+  float alpha;
+  float beta;
+  int64_t M, N, K, batch;
+  const void* A;  int64_t lda, stride_a;
+  const void* B;  int64_t ldb, stride_b;
+  const void* gY; int64_t ldgy, stride_gy;
+  const void* Z;  int64_t ldz, stride_z;
+  void* gA;       int64_t ldga, stride_ga;
+  void* gB;       int64_t ldgb, stride_gb;
+  void* gC;       int64_t ldgc, stride_gc;
+  float* gBias;   int64_t stride_gbias;
+} gev2_gemm_bwd_desc;
+
+int gev2_gemm_fwd(const gev2_gemm_fwd_desc* desc, void* stream);
+int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
+
+int gev2_abi_version(void);
+const char* gev2_status_string(int status);
+/* Message for the last failing call on this thread ("" if none). */
+const char* gev2_last_error(void);
+/* Name of the kernel family the last gev2_gemm_fwd on this thread used
+ * ("tile:<cfg>", "skinny"), for tests and profiling. */
+const char* gev2_last_path(void);
+
+/*
+ * Device, memory, stream and event helpers, so that hosts without a tensor
+ * library (the C++ binding, ctypes tests, the benchmark) can stage buffers.
+ * (The reference relies on CuPy for these.)
+ */
+int gev2_device_count(int* count);
+int gev2_set_device(int device);
+int gev2_get_device(int* device);
+/* name (NUL-terminated, truncated to name_len), compute units, peak clock kHz */
+int gev2_device_info(int device, char* name, size_t name_len, int* cu_count, int* clock_khz);
+int gev2_malloc(void** ptr, size_t bytes);
+int gev2_free(void* ptr);
+int gev2_memcpy_htod(void* dst, const void* src, size_t bytes);
+int gev2_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int gev2_memcpy_dtod_async(void* dst, const void* src, size_t bytes, void* stream);
+int gev2_memset(void* ptr, int value, size_t bytes);
+int gev2_stream_create(void** stream);
+int gev2_stream_destroy(void* stream);
+int gev2_stream_synchronize(void* stream);
+int gev2_device_synchronize(void);
+int gev2_event_create(void** event);
+int gev2_event_destroy(void* event);
+int gev2_event_record(void* event, void* stream);
+int gev2_event_synchronize(void* event);
+int gev2_event_elapsed_ms(float* ms, void* start, void* stop);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEV2_GEMM_H_ */

@@ -1,0 +1,342 @@
+"""CPU oracle for graph_executor_v2's fused GEMM + bias + activation operator.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker that the HIP path is
+compared against; it is imported by ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` and nowhere else.  The product path
+(``ai_framework-dev_amd``) never imports, calls or falls back to it.
+
+It restates, in float64 NumPy, the host math of the reference:
+
+* activation forward   -- ``backends/cuda/ops/_common/shim/activations.hpp:14-30``
+  (GELU is the tanh form with c = 0.7978845608, k1 = 0.044715 and the inner
+  argument ``fmaf(c*k1, x^3, c*x)``; Sigmoid is the branch-stable form)
+* activation derivative -- ``activations.hpp:45-70`` (LeakyReLU' is ``slope`` at
+  z == 0; the GELU derivative clamps tanh to +-0.999999)
+* epilogue             -- ``_common/shim/traits.hpp:43-71``
+  (pre = alpha*acc + bias; Z = pre; Y = act(pre))
+* bias-kind inference  -- ``_common/shim/bias.hpp:70-78`` then
+  ``backends/cuda/ops/gemm/launcher.cu:47-77``
+* backward             -- ``gemm/kernels/regemm_backward.cu:91-130,271-291``
+  (gZ = gY * act'(Z); gA = alpha*gZ B^T; gB = alpha*A^T gZ; gC = beta*gZ;
+  gBias = sum of gZ over rows / columns / everything for PerN / PerM / Scalar)
+* the reference's own NumPy test math -- ``tests/cuda_pyd_test/smoke_gemm_binding.py:84-123``
+* batched slices       -- ``backends/cuda/ops/sdpa/launcher.cu:166-170``
+  (slice (b,h) starts at ((b*H+h)*rows*cols))
+
+Parity pins (what keeps this restatement honest) live in ``tests/test_oracle.py``:
+exact-integer brute force for the GEMMs, central finite differences for every
+activation derivative and for the backward (a scalar loss), the erf form of GELU
+for the tanh approximation, and the C restatement in ``gemm_oracle.c`` (fp32,
+sequential-k ``fmaf`` -- the reference's own small-kernel order).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# Enum values (ABI anchors of the reference: _common/shim/enums.hpp:10-24,
+# ai_device.hpp:14-27)
+# ---------------------------------------------------------------------------
+ACT_NONE, ACT_RELU, ACT_LEAKY, ACT_GELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3, 4, 5
+BIAS_NONE, BIAS_SCALAR, BIAS_PERM, BIAS_PERN = 0, 1, 2, 3
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+
+GELU_C = 0.7978845608      # activations.hpp:19
+GELU_K1 = 0.044715         # activations.hpp:20
+GELU_TH_CLAMP = 0.999999   # activations.hpp:55-56
+
+_ACT_NAMES = {
+    "none": ACT_NONE, "relu": ACT_RELU, "leakyrelu": ACT_LEAKY,
+    "leaky_relu": ACT_LEAKY, "lrelu": ACT_LEAKY, "gelu": ACT_GELU,
+    "sigmoid": ACT_SIGMOID, "tanh": ACT_TANH,
+}
+
+
+def parse_act(act) -> int:
+    """String or int -> ActKind value (gemm_pybind.cpp:57-69 accepts these names)."""
+    if isinstance(act, (int, np.integer)):
+        return int(act)
+    k = str(act).lower()
+    if k not in _ACT_NAMES:
+        raise ValueError(f"unknown act: {act}")
+    return _ACT_NAMES[k]
+
+
+# ---------------------------------------------------------------------------
+# Activations (float64)
+# ---------------------------------------------------------------------------
+def act_forward(z, act, slope: float = 0.01) -> np.ndarray:
+    """act_apply<AK>(x, leaky) -- activations.hpp:14-39."""
+    a = parse_act(act)
+    z = np.asarray(z, dtype=np.float64)
+    if a == ACT_NONE:
+        return z.copy()
+    if a == ACT_RELU:
+        return np.where(z > 0.0, z, 0.0)
+    if a == ACT_LEAKY:
+        return np.where(z > 0.0, z, slope * z)
+    if a == ACT_GELU:
+        t = (GELU_C * GELU_K1) * (z * z * z) + GELU_C * z
+        return 0.5 * z * (1.0 + np.tanh(t))
+    if a == ACT_SIGMOID:
+        # branch-stable form, activations.hpp:25-29
+        e = np.exp(-np.abs(z))
+        return np.where(z >= 0.0, 1.0 / (1.0 + e), e / (1.0 + e))
+    if a == ACT_TANH:
+        return np.tanh(z)
+    raise ValueError(f"bad act {act}")
+
+
+def act_deriv(z, act, slope: float = 0.01) -> np.ndarray:
+    """act_deriv<AK>(x, leaky) -- activations.hpp:45-70."""
+    a = parse_act(act)
+    z = np.asarray(z, dtype=np.float64)
+    if a == ACT_NONE:
+        return np.ones_like(z)
+    if a == ACT_RELU:
+        return np.where(z > 0.0, 1.0, 0.0)
+    if a == ACT_LEAKY:
+        return np.where(z > 0.0, 1.0, slope)        # slope at z == 0 (:47)
+    if a == ACT_GELU:
+        x2 = z * z
+        t = (GELU_C * GELU_K1) * (x2 * z) + GELU_C * z
+        th = np.clip(np.tanh(t), -GELU_TH_CLAMP, GELU_TH_CLAMP)
+        sech2 = 1.0 - th * th
+        dt = GELU_C * (1.0 + 3.0 * GELU_K1 * x2)
+        return 0.5 * (1.0 + th) + 0.5 * z * sech2 * dt
+    if a == ACT_SIGMOID:
+        s = act_forward(z, ACT_SIGMOID)
+        return s * (1.0 - s)
+    if a == ACT_TANH:
+        th = np.tanh(z)
+        return 1.0 - th * th
+    raise ValueError(f"bad act {act}")
+
+
+# ---------------------------------------------------------------------------
+# Bias-kind inference (host logic)
+# ---------------------------------------------------------------------------
+def infer_bias_kind_1d_lenMN(shape: Optional[Sequence[int]], M: int, N: int) -> int:
+    """bias.hpp:70-78: only rank-1; len 1 -> Scalar, == N -> PerN, == M -> PerM."""
+    if shape is None or len(shape) != 1:
+        return BIAS_NONE
+    n = int(shape[0])
+    if n == 1:
+        return BIAS_SCALAR
+    if n == N:
+        return BIAS_PERN
+    if n == M:
+        return BIAS_PERM
+    return BIAS_NONE
+
+
+def infer_bias_kind_fallback(shape: Optional[Sequence[int]], M: int, N: int) -> int:
+    """gemm/launcher.cu:47-71."""
+    if shape is None:
+        return BIAS_NONE
+    s = [int(v) for v in shape]
+    if any(v < 0 for v in s):
+        return BIAS_NONE
+    numel = 1
+    for v in s:
+        numel *= v
+    if numel == 0:
+        return BIAS_NONE
+    if len(s) == 2 and s[0] == 1 and s[1] == N:
+        return BIAS_PERN
+    if len(s) == 1 and s[0] == N:
+        return BIAS_PERN
+    if len(s) == 2 and s[0] == M and s[1] == 1:
+        return BIAS_PERM
+    if len(s) == 1 and s[0] == M:
+        return BIAS_PERM
+    if (len(s) == 2 and s[0] == 1 and s[1] == 1) or (len(s) == 1 and s[0] == 1):
+        return BIAS_SCALAR
+    if numel == N:
+        return BIAS_PERN
+    if numel == M:
+        return BIAS_PERM
+    if numel == 1:
+        return BIAS_SCALAR
+    return BIAS_NONE
+
+
+def decide_bias_kind(shape: Optional[Sequence[int]], M: int, N: int) -> int:
+    """gemm/launcher.cu:73-77: strict 1-D rule first, then the fallback."""
+    k = infer_bias_kind_1d_lenMN(shape, M, N)
+    if k != BIAS_NONE:
+        return k
+    return infer_bias_kind_fallback(shape, M, N)
+
+
+def bias_add(pre: np.ndarray, bias, kind: int) -> np.ndarray:
+    """Broadcast a bias of the given kind onto pre[M,N] (bias.hpp:155-176)."""
+    if bias is None or kind == BIAS_NONE:
+        return pre
+    b = np.asarray(bias, dtype=np.float64).reshape(-1)
+    if kind == BIAS_SCALAR:
+        return pre + b[0]
+    if kind == BIAS_PERN:
+        return pre + b[None, : pre.shape[1]]
+    if kind == BIAS_PERM:
+        return pre + b[: pre.shape[0], None]
+    raise ValueError(kind)
+
+
+# ---------------------------------------------------------------------------
+# Forward / backward (float64)
+# ---------------------------------------------------------------------------
+def gemm_forward(A, B, bias=None, bias_kind: Optional[int] = None, act="none",
+                 slope: float = 0.01, alpha: float = 1.0,
+                 trans_a: bool = False, trans_b: bool = False
+                 ) -> Tuple[np.ndarray, np.ndarray]:
+    """Z = alpha * op(A) @ op(B) + bias; Y = act(Z).  Returns (Y, Z), float64."""
+    A = np.asarray(A, dtype=np.float64)
+    B = np.asarray(B, dtype=np.float64)
+    if trans_a:
+        A = A.T
+    if trans_b:
+        B = B.T
+    acc = A @ B
+    pre = acc if alpha == 1.0 else alpha * acc          # traits.hpp:44
+    if bias is not None:
+        if bias_kind is None:
+            bias_kind = decide_bias_kind(np.shape(bias), A.shape[0], B.shape[1])
+        pre = bias_add(pre, bias, bias_kind)
+    return act_forward(pre, act, slope), pre
+
+
+def gemm_backward(A, B, gY, Z, act="none", slope: float = 0.01,
+                  bias_kind: int = BIAS_NONE, alpha: float = 1.0,
+                  beta: float = 0.0) -> dict:
+    """regemm_backward.cu:91-130 (epilogue) + :271-291 (the two GEMMs), float64."""
+    A = np.asarray(A, dtype=np.float64)
+    B = np.asarray(B, dtype=np.float64)
+    gZ = np.asarray(gY, dtype=np.float64) * act_deriv(Z, act, slope)
+    out = {
+        "gZ": gZ,
+        "gA": alpha * (gZ @ B.T),
+        "gB": alpha * (A.T @ gZ),
+        "gC": beta * gZ,
+    }
+    if bias_kind == BIAS_PERN:
+        out["gBias"] = gZ.sum(axis=0)
+    elif bias_kind == BIAS_PERM:
+        out["gBias"] = gZ.sum(axis=1)
+    elif bias_kind == BIAS_SCALAR:
+        out["gBias"] = np.array([gZ.sum()])
+    else:
+        out["gBias"] = None
+    return out
+
+
+def slice_offset(b: int, h: int, H: int, rows: int, cols: int) -> int:
+    """Flat element offset of slice (b,h) -- sdpa/launcher.cu:166-170."""
+    return (b * H + h) * rows * cols
+
+
+def gemm_forward_batched(A_flat, B_flat, batch: int, M: int, N: int, K: int,
+                         sA: int, sB: int, lda: int, ldb: int,
+                         trans_b: bool = False, alpha: float = 1.0,
+                         bias=None, bias_kind: int = BIAS_NONE, sBias: int = 0,
+                         act="none", slope: float = 0.01
+                         ) -> Tuple[np.ndarray, np.ndarray]:
+    """Batched strided form over flat buffers, one slice at a time.
+
+    Slice i of A starts at ``i*sA`` (row-major, leading dimension lda);
+    B slice i at ``i*sB`` and is [K,N] (ldb) or, with trans_b, [N,K] (ldb).
+    Returns (Y, Z) as [batch, M, N] float64 arrays.
+    """
+    A_flat = np.asarray(A_flat, dtype=np.float64).reshape(-1)
+    B_flat = np.asarray(B_flat, dtype=np.float64).reshape(-1)
+    Y = np.empty((batch, M, N))
+    Z = np.empty((batch, M, N))
+    for i in range(batch):
+        a = np.lib.stride_tricks.as_strided(
+            A_flat[i * sA:], shape=(M, K), strides=(lda * 8, 8))
+        if trans_b:
+            b = np.lib.stride_tricks.as_strided(
+                B_flat[i * sB:], shape=(N, K), strides=(ldb * 8, 8)).T
+        else:
+            b = np.lib.stride_tricks.as_strided(
+                B_flat[i * sB:], shape=(K, N), strides=(ldb * 8, 8))
+        bi = None
+        if bias is not None and bias_kind != BIAS_NONE:
+            bi = np.asarray(bias, dtype=np.float64).reshape(-1)[i * sBias:]
+        Y[i], Z[i] = gemm_forward(a, b, bi, bias_kind if bi is not None else None,
+                                  act, slope, alpha)
+    return Y, Z
+
+
+# ---------------------------------------------------------------------------
+# Reduced-precision storage emulation
+# ---------------------------------------------------------------------------
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """float32 -> bf16 bit pattern, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u >> 16) & 1) + 0x7FFF
+    return ((u + r) >> 16).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_to(x, dtype: int) -> np.ndarray:
+    """Values of x (any float) after one rounding to the storage dtype, as float32."""
+    x32 = np.asarray(x, dtype=np.float32)
+    if dtype == DT_F32:
+        return x32.copy()
+    if dtype == DT_BF16:
+        return bf16_bits_to_f32(f32_to_bf16_bits(x32))
+    if dtype == DT_F16:
+        return x32.astype(np.float16).astype(np.float32)
+    raise ValueError(dtype)
+
+
+def storage_eps(dtype: int) -> float:
+    """Machine epsilon of the storage type (bf16 2^-7, fp16 2^-10, fp32 2^-23)."""
+    return {DT_F32: 2.0 ** -23, DT_BF16: 2.0 ** -7, DT_F16: 2.0 ** -10}[dtype]
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's own NumPy path (smoke_gemm_binding.py:84-123)
+# ---------------------------------------------------------------------------
+def numpy_fp32_step(A, B, bias, gY, act="relu", slope: float = 0.01):
+    """fp32 forward + backward exactly as the reference test computes it.
+
+    Used as the timed CPU baseline; float32 throughout like the reference.
+    """
+    Z = A @ B
+    if bias is not None:
+        Z = Z + bias
+    if parse_act(act) == ACT_RELU:
+        Y = np.maximum(Z, np.float32(0))
+        gZ = gY * (Z > 0)
+    else:
+        Y = act_forward(Z, act, slope).astype(np.float32)
+        gZ = (gY * act_deriv(Z, act, slope)).astype(np.float32)
+    gA = gZ @ B.T
+    gB = A.T @ gZ
+    gBias = gZ.sum(axis=0, keepdims=True)
+    return Y, Z, gA, gB, gBias
+
+
+def forward_error_bound(A, B, K: int, dtype: int, bias=None) -> np.ndarray:
+    """Componentwise bound 4*K*eps*(|A||B|)_mn + eps*|bias| for the tolerance tests."""
+    eps = storage_eps(dtype) if dtype != DT_F32 else 2.0 ** -24
+    absprod = np.abs(np.asarray(A, np.float64)) @ np.abs(np.asarray(B, np.float64))
+    bnd = 4.0 * K * eps * absprod
+    if bias is not None:
+        bnd = bnd + eps * np.abs(np.asarray(bias, np.float64))
+    return bnd
+
+
+def gelu_erf(z) -> np.ndarray:
+    """Exact GELU 0.5*z*(1+erf(z/sqrt(2))) -- what the tanh form approximates."""
+    z = np.asarray(z, dtype=np.float64)
+    erf = np.vectorize(math.erf)
+    return 0.5 * z * (1.0 + erf(z / math.sqrt(2.0)))

@@ -1,0 +1,314 @@
+"""Pins for the CPU oracle (oracle/gemm_oracle.py, oracle/gemm_oracle.c).
+
+Each check is chosen so that a plausible restatement mistake (a dropped term,
+a wrong sign, a transposed operand, a wrong special case) fails it:
+  * activations against special values, the erf form of GELU and central
+    finite differences of the forward (pins every derivative formula);
+  * GEMM forward/backward against exact integer arithmetic (Python ints);
+  * backward against finite differences of a scalar loss (pins dX/dW/dBias
+    including which operand is transposed);
+  * bias-kind inference against the reference's rules (known answers read off
+    bias.hpp:70-78 and gemm/launcher.cu:47-77);
+  * the C fp32 restatement (the reference's small-kernel summation order)
+    against the float64 one.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import gemm_oracle as O
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ACTS = ["none", "relu", "leakyrelu", "gelu", "sigmoid", "tanh"]
+
+
+# ---------------------------------------------------------------------------
+# activations
+# ---------------------------------------------------------------------------
+def test_act_special_values():
+    f = O.act_forward
+    assert f(0.0, "relu") == 0 and f(-1.0, "relu") == 0 and f(2.5, "relu") == 2.5
+    assert f(-2.0, "leakyrelu", 0.1) == pytest.approx(-0.2) and f(0.0, "leakyrelu") == 0
+    assert f(3.0, "leakyrelu", 0.1) == 3.0
+    assert f(0.0, "gelu") == 0 and f(0.0, "sigmoid") == 0.5 and f(0.0, "tanh") == 0
+    # branch-stable sigmoid: no overflow at the extremes
+    with np.errstate(over="raise"):
+        assert f(-1000.0, "sigmoid") == 0.0 and f(1000.0, "sigmoid") == 1.0
+    d = O.act_deriv
+    assert d(0.0, "relu") == 0 and d(1e-30, "relu") == 1
+    assert d(0.0, "leakyrelu", 0.2) == 0.2          # slope at z == 0 (activations.hpp:47)
+    assert d(0.0, "sigmoid") == 0.25 and d(0.0, "tanh") == 1.0
+    assert d(0.0, "gelu") == pytest.approx(0.5)
+    assert np.all(d(np.linspace(-5, 5, 11), "none") == 1.0)
+
+
+def test_gelu_tanh_form_tracks_erf_form():
+    z = np.linspace(-8, 8, 4001)
+    # the tanh approximation of GELU is within 1e-3 of the exact erf form
+    assert np.max(np.abs(O.act_forward(z, "gelu") - O.gelu_erf(z))) < 1e-3
+    # and it is *not* the erf form (the constants are the tanh ones)
+    assert np.max(np.abs(O.act_forward(z, "gelu") - O.gelu_erf(z))) > 1e-5
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_act_deriv_matches_finite_difference(act):
+    z = np.concatenate([np.linspace(-6, -0.05, 300), np.linspace(0.05, 6, 300)])
+    h = 1e-6
+    fd = (O.act_forward(z + h, act, 0.07) - O.act_forward(z - h, act, 0.07)) / (2 * h)
+    an = O.act_deriv(z, act, 0.07)
+    if act == "gelu":
+        # where the derivative's tanh clamp (activations.hpp:55-56) engages, the
+        # reference deliberately departs from d/dz of the forward; that region is
+        # pinned by test_gelu_deriv_clamp_is_applied
+        t = O.GELU_C * (z + O.GELU_K1 * z ** 3)
+        keep = np.abs(np.tanh(t)) < O.GELU_TH_CLAMP
+        assert keep.sum() > 300
+        fd, an = fd[keep], an[keep]
+    assert np.max(np.abs(fd - an)) < 2e-6
+
+
+def test_gelu_deriv_clamp_is_applied():
+    # for large |z| tanh(t) rounds to +-1; the clamp keeps sech^2 >= 1 - 0.999999^2
+    z = np.array([12.0, -12.0])
+    d = O.act_deriv(z, "gelu")
+    th = 0.999999
+    expect_pos = 0.5 * (1 + th) + 0.5 * 12.0 * (1 - th * th) * O.GELU_C * (1 + 3 * O.GELU_K1 * 144)
+    assert d[0] == pytest.approx(expect_pos, rel=1e-12)
+    assert d[0] != 1.0
+
+
+# ---------------------------------------------------------------------------
+# GEMM forward / backward
+# ---------------------------------------------------------------------------
+def _int_mat(g, r, c):
+    return g.integers(-3, 4, size=(r, c))
+
+
+def _py_matmul(A, B):
+    return [[sum(int(A[i][k]) * int(B[k][j]) for k in range(len(B))) for j in range(len(B[0]))]
+            for i in range(len(A))]
+
+
+@pytest.mark.parametrize("bias_kind", [O.BIAS_NONE, O.BIAS_PERN, O.BIAS_PERM, O.BIAS_SCALAR])
+def test_forward_exact_integers(bias_kind):
+    g = np.random.default_rng(1)
+    M, N, K = 5, 7, 6
+    A, B = _int_mat(g, M, K), _int_mat(g, K, N)
+    nb = {O.BIAS_NONE: 0, O.BIAS_PERN: N, O.BIAS_PERM: M, O.BIAS_SCALAR: 1}[bias_kind]
+    bias = g.integers(-5, 6, size=nb) if nb else None
+    Y, Z = O.gemm_forward(A, B, bias, bias_kind if nb else None, "relu", alpha=0.5)
+    ref = _py_matmul(A.tolist(), B.tolist())
+    for i in range(M):
+        for j in range(N):
+            pre = 0.5 * ref[i][j]
+            if bias_kind == O.BIAS_PERN:
+                pre += bias[j]
+            elif bias_kind == O.BIAS_PERM:
+                pre += bias[i]
+            elif bias_kind == O.BIAS_SCALAR:
+                pre += bias[0]
+            assert Z[i, j] == pre
+            assert Y[i, j] == max(pre, 0.0)
+
+
+def test_forward_transposes():
+    g = np.random.default_rng(2)
+    A, B = _int_mat(g, 4, 3), _int_mat(g, 3, 5)
+    Y0, _ = O.gemm_forward(A, B)
+    Y1, _ = O.gemm_forward(A.T.copy(), B, trans_a=True)
+    Y2, _ = O.gemm_forward(A, B.T.copy(), trans_b=True)
+    assert np.array_equal(Y0, Y1) and np.array_equal(Y0, Y2)
+    assert np.array_equal(Y0, np.array(_py_matmul(A.tolist(), B.tolist()), dtype=float))
+
+
+def test_backward_exact_integers():
+    g = np.random.default_rng(3)
+    M, N, K = 6, 4, 5
+    A, B = _int_mat(g, M, K), _int_mat(g, K, N)
+    gY = _int_mat(g, M, N)
+    _, Z = O.gemm_forward(A, B, None, None, "relu")
+    r = O.gemm_backward(A, B, gY, Z, "relu", bias_kind=O.BIAS_PERN, beta=1.0)
+    gZ = [[int(gY[i, j]) if Z[i, j] > 0 else 0 for j in range(N)] for i in range(M)]
+    BT = [list(x) for x in zip(*B.tolist())]
+    AT = [list(x) for x in zip(*A.tolist())]
+    assert np.array_equal(r["gA"], np.array(_py_matmul(gZ, BT), dtype=float))
+    assert np.array_equal(r["gB"], np.array(_py_matmul(AT, gZ), dtype=float))
+    assert np.array_equal(r["gBias"], np.array([sum(gZ[i][j] for i in range(M)) for j in range(N)], dtype=float))
+    assert np.array_equal(r["gC"], np.array(gZ, dtype=float))
+    r2 = O.gemm_backward(A, B, gY, Z, "relu", bias_kind=O.BIAS_PERM)
+    assert np.array_equal(r2["gBias"], np.array([sum(row) for row in gZ], dtype=float))
+    r3 = O.gemm_backward(A, B, gY, Z, "relu", bias_kind=O.BIAS_SCALAR)
+    assert r3["gBias"][0] == sum(map(sum, gZ))
+
+
+@pytest.mark.parametrize("act", ["gelu", "sigmoid", "tanh", "none"])
+def test_backward_matches_finite_difference(act):
+    g = np.random.default_rng(4)
+    M, N, K = 7, 5, 6
+    X, W = g.standard_normal((M, K)), g.standard_normal((K, N)) / 2
+    b = g.standard_normal(N) / 3
+    G = g.standard_normal((M, N))
+
+    def loss(X_, W_, b_):
+        Y, _ = O.gemm_forward(X_, W_, b_, O.BIAS_PERN, act)
+        return float(np.sum(G * Y))
+
+    _, Z = O.gemm_forward(X, W, b, O.BIAS_PERN, act)
+    r = O.gemm_backward(X, W, G, Z, act, bias_kind=O.BIAS_PERN)
+    h = 1e-6
+    for name, base, grad in (("X", X, r["gA"]), ("W", W, r["gB"]), ("b", b, r["gBias"])):
+        D = g.standard_normal(base.shape)
+        args_p = [X, W, b]
+        args_m = [X, W, b]
+        idx = {"X": 0, "W": 1, "b": 2}[name]
+        args_p[idx] = base + h * D
+        args_m[idx] = base - h * D
+        fd = (loss(*args_p) - loss(*args_m)) / (2 * h)
+        assert fd == pytest.approx(float(np.sum(grad * D)), rel=1e-6, abs=1e-8), name
+
+
+def test_batched_slice_offsets():
+    """Slice (b,h) of a [B,H,R,C] buffer starts at ((b*H+h)*R*C) (sdpa/launcher.cu:166-170)."""
+    B, H, R, C = 2, 3, 4, 5
+    flat = np.arange(B * H * R * C)
+    t = flat.reshape(B, H, R, C)
+    for b in range(B):
+        for h in range(H):
+            off = O.slice_offset(b, h, H, R, C)
+            assert np.array_equal(flat[off:off + R * C].reshape(R, C), t[b, h])
+
+
+def test_batched_forward_matches_loop():
+    g = np.random.default_rng(5)
+    batch, M, N, K = 3, 4, 6, 5
+    lda, ldb = K + 2, K + 1
+    sA, sB = M * lda + 3, N * ldb
+    A = g.integers(-2, 3, batch * sA).astype(float)
+    Bf = g.integers(-2, 3, batch * sB).astype(float)
+    Y, _ = O.gemm_forward_batched(A, Bf, batch, M, N, K, sA, sB, lda, ldb, trans_b=True, alpha=0.25)
+    for i in range(batch):
+        a = A[i * sA:i * sA + M * lda].reshape(M, lda)[:, :K]
+        bt = Bf[i * sB:i * sB + N * ldb].reshape(N, ldb)[:, :K]
+        assert np.array_equal(Y[i], 0.25 * (a @ bt.T))
+
+
+# ---------------------------------------------------------------------------
+# bias-kind inference
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,M,N,expect", [
+    ((8,), 4, 8, O.BIAS_PERN),
+    ((4,), 4, 8, O.BIAS_PERM),
+    ((1,), 4, 8, O.BIAS_SCALAR),
+    ((8,), 8, 8, O.BIAS_PERN),        # PerN wins when M == N (bias.hpp:76-77)
+    ((1,), 1, 1, O.BIAS_SCALAR),      # Scalar wins over everything
+    ((1, 8), 4, 8, O.BIAS_PERN),      # 2-D forms via the fallback (launcher.cu:60-65)
+    ((4, 1), 4, 8, O.BIAS_PERM),
+    ((1, 1), 4, 8, O.BIAS_SCALAR),
+    ((2, 4), 4, 8, O.BIAS_PERN),      # numel == N (launcher.cu:67)
+    ((2, 2), 4, 8, O.BIAS_PERM),      # numel == M (launcher.cu:68)
+    ((4, 8), 4, 8, O.BIAS_NONE),      # (M,N): silently no bias (launcher.cu:70)
+    ((0,), 4, 8, O.BIAS_NONE),
+    ((3,), 4, 8, O.BIAS_NONE),
+    (None, 4, 8, O.BIAS_NONE),
+])
+def test_decide_bias_kind(shape, M, N, expect):
+    assert O.decide_bias_kind(shape, M, N) == expect
+
+
+# ---------------------------------------------------------------------------
+# reduced precision emulation
+# ---------------------------------------------------------------------------
+def test_bf16_rounding_known_answers():
+    one = 1.0
+    x = np.array([one, one + 2 ** -8, one + 3 * 2 ** -8, -2.5, 3.0e38, 1e-40], np.float32)
+    r = O.round_to(x, O.DT_BF16)
+    assert r[0] == 1.0
+    assert r[1] == 1.0                      # tie -> even
+    assert r[2] == 1.0 + 2 ** -6            # tie -> even (odd neighbour rounds up)
+    assert r[3] == -2.5
+    assert np.isfinite(r[4])
+    assert np.array_equal(O.round_to(np.float32(1.5), O.DT_F16), np.float32(1.5))
+    assert O.round_to(np.float32(1 + 2 ** -11), O.DT_F16) == 1.0
+
+
+# ---------------------------------------------------------------------------
+# C restatement (fp32, reference small-kernel order)
+# ---------------------------------------------------------------------------
+def _load_c_oracle():
+    path = os.path.join(REPO, "oracle", "libgemm_oracle.so")
+    if not os.path.exists(path):
+        import subprocess
+        subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle")], check=True)
+    L = ctypes.CDLL(path)
+    f = ctypes.POINTER(ctypes.c_float)
+    i64 = ctypes.c_int64
+    L.gev2o_gemm_fwd_f32.argtypes = [i64, i64, i64, f, i64, f, i64, f, ctypes.c_int, ctypes.c_float,
+                                     ctypes.c_int, ctypes.c_float, f, i64, f, i64]
+    L.gev2o_act_array.argtypes = [f, f, i64, ctypes.c_int, ctypes.c_float]
+    L.gev2o_act_deriv_array.argtypes = [f, f, i64, ctypes.c_int, ctypes.c_float]
+    L.gev2o_gemm_bwd_f32.argtypes = [i64, i64, i64, f, i64, f, i64, f, i64, f, i64, ctypes.c_int,
+                                     ctypes.c_float, ctypes.c_float, ctypes.c_float, f, i64, f, i64,
+                                     f, i64, f, ctypes.c_int, f]
+    return L
+
+
+def _fp(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_c_oracle_activations(act):
+    L = _load_c_oracle()
+    x = np.linspace(-7, 7, 1001).astype(np.float32)
+    y = np.empty_like(x)
+    d = np.empty_like(x)
+    a = O.parse_act(act)
+    L.gev2o_act_array(_fp(x), _fp(y), x.size, a, 0.05)
+    L.gev2o_act_deriv_array(_fp(x), _fp(d), x.size, a, 0.05)
+    assert np.max(np.abs(y - O.act_forward(x, act, 0.05))) < 4e-6
+    assert np.max(np.abs(d - O.act_deriv(x, act, 0.05))) < 4e-6
+
+
+def test_c_oracle_forward_and_backward():
+    L = _load_c_oracle()
+    g = np.random.default_rng(6)
+    M, N, K = 33, 21, 47
+    X = (g.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    W = g.standard_normal((K, N)).astype(np.float32)
+    b = g.standard_normal(N).astype(np.float32)
+    Y = np.empty((M, N), np.float32)
+    Z = np.empty((M, N), np.float32)
+    L.gev2o_gemm_fwd_f32(M, N, K, _fp(X), K, _fp(W), N, _fp(b), O.BIAS_PERN, 1.0, O.ACT_GELU, 0.01,
+                         _fp(Y), N, _fp(Z), N)
+    Y64, Z64 = O.gemm_forward(X, W, b, O.BIAS_PERN, "gelu")
+    bound = 1.01 * K * 2.0 ** -24 * (np.abs(X.astype(float)) @ np.abs(W.astype(float))) + 1e-6
+    assert np.all(np.abs(Z - Z64) <= bound)
+    assert np.all(np.abs(Y - Y64) <= 1.2 * bound + 1e-6)
+    gY = g.standard_normal((M, N)).astype(np.float32)
+    gA = np.empty((M, K), np.float32)
+    gB = np.empty((K, N), np.float32)
+    gC = np.empty((M, N), np.float32)
+    gb = np.empty(N, np.float32)
+    tmp = np.empty((M, N), np.float32)
+    L.gev2o_gemm_bwd_f32(M, N, K, _fp(X), K, _fp(W), N, _fp(gY), N, _fp(Z), N, O.ACT_GELU, 0.01,
+                         1.0, 1.0, _fp(gA), K, _fp(gB), N, _fp(gC), N, _fp(gb), O.BIAS_PERN, _fp(tmp))
+    r = O.gemm_backward(X, W, gY, Z, "gelu", bias_kind=O.BIAS_PERN, beta=1.0)
+    for name, dev in (("gA", gA), ("gB", gB), ("gC", gC), ("gBias", gb)):
+        ref = r[name]
+        assert np.max(np.abs(dev - ref)) <= 1e-5 * (1 + np.max(np.abs(ref))), name
+
+
+def test_numpy_baseline_matches_oracle():
+    g = np.random.default_rng(8)
+    X = g.standard_normal((16, 24)).astype(np.float32)
+    W = g.standard_normal((24, 12)).astype(np.float32)
+    b = g.standard_normal((1, 12)).astype(np.float32)
+    gY = g.standard_normal((16, 12)).astype(np.float32)
+    Y, Z, gA, gB, gb = O.numpy_fp32_step(X, W, b, gY, "relu")
+    Y64, Z64 = O.gemm_forward(X, W, b[0], O.BIAS_PERN, "relu")
+    r = O.gemm_backward(X, W, gY, Z, "relu", bias_kind=O.BIAS_PERN)
+    assert np.allclose(Y, Y64, atol=1e-5) and np.allclose(gA, r["gA"], atol=1e-4)
+    assert np.allclose(gB, r["gB"], atol=1e-4) and np.allclose(gb[0], r["gBias"], atol=1e-4)
