@@ -3,6 +3,7 @@
 // gemm_aux.hip.  Nothing here throws across the ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -51,15 +52,30 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Vector (16-byte) loads of an operand are legal when its base is 16-byte
 // aligned and every row start and every chunk start is too.
-bool vec_ok(const void* p, int64_t ld, int64_t stride, int64_t contig_extent, int batch, int dtype) {
+// The vector path also addresses each operand slice with 32-bit byte offsets
+// from the slice origin (raw buffer loads), so a slice must span < 2^31 bytes.
+bool vec_ok(const void* p, int64_t ld, int64_t stride, int64_t contig_extent, int64_t rows, int batch,
+            int dtype) {
   if (!p) return true;
   const int epc = elems_per_chunk(dtype);
   if (!aligned16(p) || ld % epc != 0 || contig_extent % epc != 0) return false;
   if (batch > 1 && stride % epc != 0) return false;
+  const int64_t span = (rows > 0 ? (rows - 1) * ld : 0) + contig_extent;
+  if (span * static_cast<int64_t>(elem_size(dtype)) > 0x7fffff00LL) return false;
   return true;
 }
 
 bool fits_i32(int64_t v) { return v >= 0 && v <= 0x7fffffffLL; }
+
+// Vector epilogue: 4-column groups (whole, N % 4 == 0) at 16-byte aligned
+// rows, written with 32-bit offsets from the slice origin (< 2^31 bytes).
+bool out_vec_ok(const void* p, int64_t ld, int64_t stride, int64_t rows, int64_t cols, int batch, int dtype) {
+  if (!p) return true;
+  if (!aligned16(p) || ld % 4 != 0 || cols % 4 != 0) return false;
+  if (batch > 1 && stride % 4 != 0) return false;
+  const int64_t span = (rows > 0 ? (rows - 1) * ld : 0) + cols;
+  return span * static_cast<int64_t>(elem_size(dtype)) <= 0x7fffff00LL;
+}
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
@@ -67,19 +83,35 @@ int env_int(const char* name, int dflt) {
   return std::atoi(v);
 }
 
-// Tile configuration heuristic: largest tile that still gives the 256 CUs at
-// least one workgroup each; GEV2_TILE_CFG overrides (tuning runs).
-int pick_cfg(int dtype, int64_t M, int64_t N, int64_t batch) {
+// Tile configuration: the candidate with the least estimated time, where a
+// launch takes ceil(workgroups / (256 CUs x workgroups resident per CU))
+// rounds, and a round costs (workgroups sharing a CU x tile area) divided by a
+// per-size MFMA efficiency (larger tiles reuse more of each LDS fragment).
+// GEV2_TILE_CFG overrides it (tuning runs).
+// `fused` (an act' prologue on one operand) excludes 256x256: its extra
+// operand registers would spill with 256 accumulators per lane.
+int pick_cfg(int dtype, int64_t M, int64_t N, int64_t batch, bool fused = false) {
   const int forced = env_int("GEV2_TILE_CFG", -1);
-  if (forced >= 0) return forced;
-  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-  if (dtype != GEV2_F32) {
-    if (tiles(128, 256) >= 256) return gev2::kCfg128x256;
-    if (tiles(128, 128) >= 192) return gev2::kCfg128x128;
-    return gev2::kCfg64x64;
+  if (forced >= 0) return (fused && forced == gev2::kCfg256x256) ? gev2::kCfg128x256 : forced;
+  struct Cand { int cfg, bm, bn, per_cu; double eff; };
+  static const Cand cands[] = {
+      {gev2::kCfg256x256, 256, 256, 1, 1.0},
+      {gev2::kCfg128x256, 128, 256, 1, 0.85},
+      {gev2::kCfg128x128, 128, 128, 2, 0.7},
+      {gev2::kCfg64x64, 64, 64, 4, 0.35},
+  };
+  (void)dtype;
+  int best = gev2::kCfg64x64;
+  double best_cost = 1e300;
+  for (const Cand& c : cands) {
+    if (fused && c.cfg == gev2::kCfg256x256) continue;
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+    const int64_t rounds = (tiles + 256 * c.per_cu - 1) / (256 * c.per_cu);
+    const int64_t resident = std::min<int64_t>(c.per_cu, (tiles + 255) / 256);
+    const double cost = static_cast<double>(rounds) * resident * c.bm * c.bn / c.eff;
+    if (cost < best_cost * 0.999) { best_cost = cost; best = c.cfg; }
   }
-  if (tiles(128, 128) >= 256) return gev2::kCfg128x128;
-  return gev2::kCfg64x64;
+  return best;
 }
 
 const char* cfg_name(int cfg, bool vec) {
@@ -133,6 +165,28 @@ int get_skinny_ws(hipStream_t s, size_t partial_bytes, size_t counters, SkinnyWs
     ws.counter_count = counters;
   }
   *out = &ws;
+  return GEV2_OK;
+}
+
+// dY' workspace of the backward for non-linear activations, one per
+// (device, stream), grown on demand.  hipFree waits for queued work that may
+// still read the old buffer.
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_grad_ws;
+
+int get_grad_ws(hipStream_t s, size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto& ws = g_grad_ws[{dev, s}];
+  if (ws.second < bytes) {
+    if (ws.first) (void)hipFree(ws.first);
+    ws = {nullptr, 0};
+    e = hipMalloc(&ws.first, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(dY' workspace)");
+    ws.second = bytes;
+  }
+  *out = ws.first;
   return GEV2_OK;
 }
 
@@ -200,7 +254,7 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   // ---- skinny path ----
   const int epc = elems_per_chunk(d->dtype);
   const bool skinny_ok = batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 &&
-                         N % epc == 0 && vec_ok(d->B, ldb, 0, N, 1, d->dtype) &&
+                         N % epc == 0 && vec_ok(d->B, ldb, 0, N, K, 1, d->dtype) &&
                          env_int("GEV2_NO_SKINNY", 0) == 0;
   if (skinny_ok) {
     const int slab = gev2::skinny_slab_cols(d->dtype);
@@ -232,8 +286,8 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   }
 
   // ---- tile path ----
-  const bool vec = vec_ok(d->A, lda, d->stride_a, ta ? M : K, batch, d->dtype) &&
-                   vec_ok(d->B, ldb, d->stride_b, tb ? K : N, batch, d->dtype) &&
+  const bool vec = vec_ok(d->A, lda, d->stride_a, ta ? M : K, ta ? K : M, batch, d->dtype) &&
+                   vec_ok(d->B, ldb, d->stride_b, tb ? K : N, tb ? N : K, batch, d->dtype) &&
                    env_int("GEV2_SCALAR_LOADS", 0) == 0;
   const int cfg = pick_cfg(d->dtype, M, N, batch);
   gev2::TileArgs a{};
@@ -248,9 +302,8 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
   a.tiles_m = static_cast<int>((M + bm - 1) / bm);
   a.tiles_n = static_cast<int>((N + bn - 1) / bn);
-  a.store_vec = (aligned16(d->Y) && ldy % 4 == 0 && (batch == 1 || d->stride_y % 4 == 0) &&
-                 (!d->Z || (aligned16(d->Z) && ldz % 4 == 0 && (batch == 1 || d->stride_z % 4 == 0))))
-                    ? 1 : 0;
+  a.store_vec = (out_vec_ok(d->Y, ldy, d->stride_y, M, N, batch, d->dtype) &&
+                 out_vec_ok(d->Z, ldz, d->stride_z, M, N, batch, d->dtype)) ? 1 : 0;
   if (static_cast<int64_t>(a.tiles_m) * a.tiles_n > 0x7fffffffLL || batch > 65535)
     return fail(GEV2_INVALID, "grid too large");
   hipError_t e = gev2::launch_tile(d->dtype, cfg, ta, tb, 0, vec, a, batch, s);
@@ -280,19 +333,47 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int dt = d->dtype;
+  const int64_t es = static_cast<int64_t>(elem_size(dt));
   const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
-  const bool fuse_bias = want_bias && d->bias_kind == GEV2_BIAS_PER_N && d->gB != nullptr;
-  const bool gyz_vec = vec_ok(d->gY, ldgy, d->stride_gy, N, batch, dt) &&
-                       vec_ok(d->Z, ldz, d->stride_z, N, batch, dt) &&
-                       env_int("GEV2_SCALAR_LOADS", 0) == 0;
+  const bool scalar_loads = env_int("GEV2_SCALAR_LOADS", 0) != 0;
 
-  // gA[M,K] = alpha * (gY (.) act'(Z)) [M,N] * B^T : NT, prologue on A
+  // dY' operand of the two GEMMs: gY with act'(Z) applied while loading
+  // (piecewise-linear activations), or gZ materialised once in a workspace.
+  const bool linear = d->act == GEV2_ACT_NONE || d->act == GEV2_ACT_RELU || d->act == GEV2_ACT_LEAKY_RELU;
+  const void* G = d->gY;
+  int64_t ldG = ldgy, sG = d->stride_gy;
+  bool fused = true;
+  if (!linear && (d->gA || d->gB)) {
+    const int64_t need = static_cast<int64_t>(batch) * M * N * es;
+    void* ws = nullptr;
+    if (d->workspace && d->workspace_bytes >= need && aligned16(d->workspace)) {
+      ws = d->workspace;
+    } else {
+      st = get_grad_ws(s, static_cast<size_t>(need), &ws);
+      if (st != GEV2_OK) return st;
+    }
+    gev2::GradArgs g{};
+    g.gY = d->gY; g.Z = d->Z; g.out = ws; g.gbias = nullptr;
+    g.ldgy = ldgy; g.ldz = ldz; g.ldout = N;
+    g.sgY = d->stride_gy; g.sZ = d->stride_z; g.sOut = M * N; g.sGbias = 0;
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N);
+    g.act = d->act; g.slope = d->leaky_slope; g.beta = 1.0f; g.bias_kind = GEV2_BIAS_NONE;
+    hipError_t e = gev2::launch_grad_elementwise(dt, g, batch, s);
+    if (e != hipSuccess) return hip_fail(e, "gZ launch");
+    G = ws; ldG = N; sG = M * N;
+    fused = false;
+  }
+  const bool fuse_bias = fused && want_bias && d->bias_kind == GEV2_BIAS_PER_N && d->gB != nullptr;
+  const bool gyz_vec = vec_ok(G, ldG, sG, N, M, batch, dt) &&
+                       (!fused || vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt)) && !scalar_loads;
+
+  // gA[M,K] = alpha * dY' [M,N] * B^T : NT (prologue on A when fused)
   if (d->gA) {
-    const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, batch, dt);
-    const int cfg = pick_cfg(dt, M, K, batch);
+    const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, K, batch, dt);
+    const int cfg = pick_cfg(dt, M, K, batch, fused);
     gev2::TileArgs a{};
-    a.A = d->gY; a.lda = ldgy; a.sA = d->stride_gy;
-    a.Zi = d->Z; a.ldzi = ldz; a.sZi = d->stride_z;
+    a.A = G; a.lda = ldG; a.sA = sG;
+    a.Zi = fused ? d->Z : nullptr; a.ldzi = ldz; a.sZi = d->stride_z;
     a.B = d->B; a.ldb = ldb; a.sB = d->stride_b;
     a.D = d->gA; a.ldd = ldga; a.sD = d->stride_ga;
     a.M = static_cast<int>(M); a.N = static_cast<int>(K); a.K = static_cast<int>(N);
@@ -301,18 +382,18 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
     a.tiles_m = static_cast<int>((M + bm - 1) / bm);
     a.tiles_n = static_cast<int>((K + bn - 1) / bn);
-    a.store_vec = (aligned16(d->gA) && ldga % 4 == 0 && (batch == 1 || d->stride_ga % 4 == 0)) ? 1 : 0;
-    hipError_t e = gev2::launch_tile(dt, cfg, false, true, 1, vec, a, batch, s);
+    a.store_vec = out_vec_ok(d->gA, ldga, d->stride_ga, M, K, batch, dt) ? 1 : 0;
+    hipError_t e = gev2::launch_tile(dt, cfg, false, true, fused ? 1 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dX launch");
   }
-  // gB[K,N] = alpha * A^T [K,M] * (gY (.) act'(Z)) [M,N] : TN, prologue on B (+ dBias)
+  // gB[K,N] = alpha * A^T [K,M] * dY' [M,N] : TN (prologue on B + fused dBias when fused)
   if (d->gB) {
-    const bool vec = gyz_vec && vec_ok(d->A, lda, d->stride_a, K, batch, dt);
-    const int cfg = pick_cfg(dt, K, N, batch);
+    const bool vec = gyz_vec && vec_ok(d->A, lda, d->stride_a, K, M, batch, dt);
+    const int cfg = pick_cfg(dt, K, N, batch, fused);
     gev2::TileArgs a{};
     a.A = d->A; a.lda = lda; a.sA = d->stride_a;
-    a.B = d->gY; a.ldb = ldgy; a.sB = d->stride_gy;
-    a.Zi = d->Z; a.ldzi = ldz; a.sZi = d->stride_z;
+    a.B = G; a.ldb = ldG; a.sB = sG;
+    a.Zi = fused ? d->Z : nullptr; a.ldzi = ldz; a.sZi = d->stride_z;
     a.D = d->gB; a.ldd = ldgb; a.sD = d->stride_gb;
     a.dbias = fuse_bias ? d->gBias : nullptr; a.sDbias = d->stride_gbias;
     a.M = static_cast<int>(K); a.N = static_cast<int>(N); a.K = static_cast<int>(M);
@@ -321,8 +402,8 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
     a.tiles_m = static_cast<int>((K + bm - 1) / bm);
     a.tiles_n = static_cast<int>((N + bn - 1) / bn);
-    a.store_vec = (aligned16(d->gB) && ldgb % 4 == 0 && (batch == 1 || d->stride_gb % 4 == 0)) ? 1 : 0;
-    hipError_t e = gev2::launch_tile(dt, cfg, true, false, 2, vec, a, batch, s);
+    a.store_vec = out_vec_ok(d->gB, ldgb, d->stride_gb, K, N, batch, dt) ? 1 : 0;
+    hipError_t e = gev2::launch_tile(dt, cfg, true, false, fused ? 2 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dW launch");
   }
   if (d->gC || (want_bias && !fuse_bias)) {
@@ -340,6 +421,24 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       hipError_t e = gev2::launch_bias_grad(dt, g, batch, s);
       if (e != hipSuccess) return hip_fail(e, "bias-grad launch");
     }
+  }
+  return GEV2_OK;
+}
+
+int gev2_gemm_fwd_repeat(const gev2_gemm_fwd_desc* descs, int n_descs, int reps, void* stream) {
+  if (!descs || n_descs < 1 || reps < 0) return fail(GEV2_INVALID_ARGUMENT, "bad repeat arguments");
+  for (int i = 0; i < reps; ++i) {
+    const int st = gev2_gemm_fwd(descs + (i % n_descs), stream);
+    if (st != GEV2_OK) return st;
+  }
+  return GEV2_OK;
+}
+
+int gev2_gemm_bwd_repeat(const gev2_gemm_bwd_desc* descs, int n_descs, int reps, void* stream) {
+  if (!descs || n_descs < 1 || reps < 0) return fail(GEV2_INVALID_ARGUMENT, "bad repeat arguments");
+  for (int i = 0; i < reps; ++i) {
+    const int st = gev2_gemm_bwd(descs + (i % n_descs), stream);
+    if (st != GEV2_OK) return st;
   }
   return GEV2_OK;
 }
@@ -416,6 +515,15 @@ int gev2_stream_destroy(void* stream) {
         if (it->second.partial) (void)hipFree(it->second.partial);
         if (it->second.counters) (void)hipFree(it->second.counters);
         it = g_ws.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    for (auto it = g_grad_ws.begin(); it != g_grad_ws.end();) {
+      if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
+        (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+        if (it->second.first) (void)hipFree(it->second.first);
+        it = g_grad_ws.erase(it);
       } else {
         ++it;
       }

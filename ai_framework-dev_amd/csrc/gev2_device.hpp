@@ -160,6 +160,17 @@ __device__ __forceinline__ void dispatch_act(int act, F&& f) {
   }
 }
 
+// Run-time choice among the piecewise-linear activations only (none, ReLU,
+// LeakyReLU); any other kind is treated as none.
+template <typename F>
+__device__ __forceinline__ void dispatch_act_linear(int act, F&& f) {
+  switch (act) {
+    case kActRelu: f.template operator()<kActRelu>(); break;
+    case kActLeaky: f.template operator()<kActLeaky>(); break;
+    default: f.template operator()<kActNone>(); break;
+  }
+}
+
 __device__ __forceinline__ float load_bias(const float* bias, int kind, int m, int n) {
   switch (kind) {
     case kBiasScalar: return bias[0];

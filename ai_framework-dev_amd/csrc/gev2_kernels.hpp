@@ -60,7 +60,7 @@ struct GradArgs {
 // Launcher entry points (each returns hipError_t from the launch).
 // Tile configuration ids, chosen by the host dispatcher.
 enum TileCfg : int {
-  kCfg256x256 = 0,   // 16-bit: 256x256x64 tile, 8 waves (128x64 per wave)
+  kCfg256x256 = 0,   // 256x256, 4 waves (128x128 per wave)
   kCfg128x128 = 1,   // 128x128, 4 waves (64x64 per wave)
   kCfg64x64 = 2,     // 64x64, 4 waves (32x32 per wave)
   kCfg128x256 = 3,   // 128x256, 4 waves (64x128 per wave)

@@ -258,6 +258,11 @@ static Status backward_impl(const Tensor& A, const Tensor& B, const Tensor* C, c
   d.gC = gC ? gC->data : nullptr; d.ldgc = ldgc; d.stride_gc = bt.stride_gc;
   d.gBias = bk != BiasKind::None ? static_cast<float*>(gBias->data) : nullptr;
   d.stride_gbias = bt.stride_gbias;
+  if (ws && ws->scratch) {   // the reference's dZ scratch (M*N fp32) doubles as gZ storage
+    d.workspace = ws->scratch;
+    d.workspace_bytes = static_cast<int64_t>(ws->scratch_bytes ? ws->scratch_bytes
+                                                                : GemmRequiredBackwardScratchBytes(M, N));
+  }
   return from_abi(gev2_gemm_bwd(&d, stream));
 }
 

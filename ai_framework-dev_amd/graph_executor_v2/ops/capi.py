@@ -20,7 +20,7 @@ ACT = {"none": 0, "relu": 1, "leakyrelu": 2, "leaky_relu": 2, "lrelu": 2, "gelu"
 BIAS_NONE, BIAS_SCALAR, BIAS_PERM, BIAS_PERN = 0, 1, 2, 3
 
 EXPORTED = [
-    "gev2_gemm_fwd", "gev2_gemm_bwd", "gev2_abi_version", "gev2_status_string",
+    "gev2_gemm_fwd", "gev2_gemm_bwd", "gev2_gemm_fwd_repeat", "gev2_gemm_bwd_repeat", "gev2_abi_version", "gev2_status_string",
     "gev2_last_error", "gev2_last_path", "gev2_device_count", "gev2_set_device",
     "gev2_get_device", "gev2_device_info", "gev2_malloc", "gev2_free", "gev2_memcpy_htod",
     "gev2_memcpy_dtoh", "gev2_memcpy_dtod_async", "gev2_memset", "gev2_stream_create",
@@ -57,6 +57,7 @@ class BwdDesc(ctypes.Structure):
         ("gB", ctypes.c_void_p), ("ldgb", ctypes.c_int64), ("stride_gb", ctypes.c_int64),
         ("gC", ctypes.c_void_p), ("ldgc", ctypes.c_int64), ("stride_gc", ctypes.c_int64),
         ("gBias", ctypes.c_void_p), ("stride_gbias", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -82,6 +83,8 @@ def lib() -> ctypes.CDLL:
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     L.gev2_gemm_fwd.argtypes = [ctypes.POINTER(FwdDesc), vp]
     L.gev2_gemm_bwd.argtypes = [ctypes.POINTER(BwdDesc), vp]
+    L.gev2_gemm_fwd_repeat.argtypes = [ctypes.POINTER(FwdDesc), i32, i32, vp]
+    L.gev2_gemm_bwd_repeat.argtypes = [ctypes.POINTER(BwdDesc), i32, i32, vp]
     for f in ("gev2_status_string",):
         getattr(L, f).restype = ctypes.c_char_p
         getattr(L, f).argtypes = [i32]
@@ -229,12 +232,12 @@ def device_count() -> int:
 # ---------------------------------------------------------------------------
 # Operator calls
 # ---------------------------------------------------------------------------
-def gemm_fwd(*, dtype: int, M: int, N: int, K: int, A: int, B: int, Y: int,
+def fwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, Y: int,
              bias: int = 0, bias_kind: int = BIAS_NONE, Z: int = 0, act="none",
              leaky_slope: float = 0.01, alpha: float = 1.0, trans_a: bool = False,
              trans_b: bool = False, batch: int = 1, lda: int = 0, ldb: int = 0, ldy: int = 0,
              ldz: int = 0, stride_a: int = 0, stride_b: int = 0, stride_y: int = 0,
-             stride_z: int = 0, stride_bias: int = 0, stream: int = 0) -> None:
+             stride_z: int = 0, stride_bias: int = 0) -> FwdDesc:
     d = FwdDesc()
     d.dtype, d.act, d.bias_kind = dtype, ACT[act] if isinstance(act, str) else int(act), bias_kind
     d.trans_a, d.trans_b = int(trans_a), int(trans_b)
@@ -245,16 +248,17 @@ def gemm_fwd(*, dtype: int, M: int, N: int, K: int, A: int, B: int, Y: int,
     d.bias, d.stride_bias = bias or None, stride_bias
     d.Y, d.ldy, d.stride_y = Y or None, ldy, stride_y
     d.Z, d.ldz, d.stride_z = Z or None, ldz, stride_z
-    check(lib().gev2_gemm_fwd(ctypes.byref(d), stream or None), "gev2_gemm_fwd")
+    return d
 
 
-def gemm_bwd(*, dtype: int, M: int, N: int, K: int, A: int, B: int, gY: int, Z: int,
+def bwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, gY: int, Z: int,
              gA: int = 0, gB: int = 0, gC: int = 0, gBias: int = 0, bias_kind: int = BIAS_NONE,
              act="none", leaky_slope: float = 0.01, alpha: float = 1.0, beta: float = 0.0,
              batch: int = 1, lda: int = 0, ldb: int = 0, ldgy: int = 0, ldz: int = 0,
              ldga: int = 0, ldgb: int = 0, ldgc: int = 0, stride_a: int = 0, stride_b: int = 0,
              stride_gy: int = 0, stride_z: int = 0, stride_ga: int = 0, stride_gb: int = 0,
-             stride_gc: int = 0, stride_gbias: int = 0, stream: int = 0) -> None:
+             stride_gc: int = 0, stride_gbias: int = 0, workspace: int = 0,
+             workspace_bytes: int = 0) -> BwdDesc:
     d = BwdDesc()
     d.dtype, d.act, d.bias_kind = dtype, ACT[act] if isinstance(act, str) else int(act), bias_kind
     d.leaky_slope, d.alpha, d.beta = leaky_slope, alpha, beta
@@ -267,7 +271,29 @@ def gemm_bwd(*, dtype: int, M: int, N: int, K: int, A: int, B: int, gY: int, Z: 
     d.gB, d.ldgb, d.stride_gb = gB or None, ldgb, stride_gb
     d.gC, d.ldgc, d.stride_gc = gC or None, ldgc, stride_gc
     d.gBias, d.stride_gbias = gBias or None, stride_gbias
+    d.workspace, d.workspace_bytes = workspace or None, workspace_bytes
+    return d
+
+
+def gemm_fwd(*, stream: int = 0, **kw) -> None:
+    d = fwd_desc(**kw)
+    check(lib().gev2_gemm_fwd(ctypes.byref(d), stream or None), "gev2_gemm_fwd")
+
+
+def gemm_bwd(*, stream: int = 0, **kw) -> None:
+    d = bwd_desc(**kw)
     check(lib().gev2_gemm_bwd(ctypes.byref(d), stream or None), "gev2_gemm_bwd")
+
+
+def gemm_fwd_repeat(descs, reps: int, stream: int = 0) -> None:
+    """reps back-to-back forward calls issued from C, cycling through descs."""
+    arr = (FwdDesc * len(descs))(*descs)
+    check(lib().gev2_gemm_fwd_repeat(arr, len(descs), reps, stream or None), "gev2_gemm_fwd_repeat")
+
+
+def gemm_bwd_repeat(descs, reps: int, stream: int = 0) -> None:
+    arr = (BwdDesc * len(descs))(*descs)
+    check(lib().gev2_gemm_bwd_repeat(arr, len(descs), reps, stream or None), "gev2_gemm_bwd_repeat")
 
 
 # ---------------------------------------------------------------------------

@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra configs to run")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return ap.parse_args()
 
 
@@ -66,6 +69,23 @@ class Ctx:
         for b in self.bufs:
             b.free()
         self.bufs = []
+
+    def time_repeat(self, descs, iters, kind="fwd", warmup=3):
+        """Average ms per launch of `iters` back-to-back calls issued from C
+        (gev2_gemm_*_repeat), cycling through descs; HIP events on self.stream."""
+        capi = self.capi
+        rep = capi.gemm_fwd_repeat if kind == "fwd" else capi.gemm_bwd_repeat
+        rep(descs, warmup, self.stream.ptr)
+        self.stream.synchronize()
+        e0, e1 = capi.Event(), capi.Event()
+        e0.record(self.stream.ptr)
+        rep(descs, iters, self.stream.ptr)
+        e1.record(self.stream.ptr)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / iters
+        e0.destroy()
+        e1.destroy()
+        return ms
 
     def time_ms(self, fn, iters, warmup=3):
         """Average ms per call of fn() (which launches on self.stream)."""
@@ -102,20 +122,16 @@ def headline(ctx, steps, warmup, dtype, M=4096, N=4096, K=4096, seed=3):
     pY, pZ = ctx.empty(M * N * es), ctx.empty(M * N * es)
     pgA, pgB, pgb = ctx.empty(M * K * es), ctx.empty(K * N * es), ctx.empty(N * 4)
     s = ctx.stream.ptr
-
-    def fwd():
-        capi.gemm_fwd(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
-                      bias_kind=capi.BIAS_PERN, act="relu", stream=s)
-
-    def bwd():
-        capi.gemm_bwd(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
-                      gBias=pgb, bias_kind=capi.BIAS_PERN, act="relu", stream=s)
+    fd = capi.fwd_desc(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
+                       bias_kind=capi.BIAS_PERN, act="relu")
+    bd = capi.bwd_desc(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
+                       gBias=pgb, bias_kind=capi.BIAS_PERN, act="relu")
 
     def step():
-        fwd()
-        bwd()
+        capi.gemm_fwd_repeat([fd], 1, s)
+        capi.gemm_bwd_repeat([bd], 1, s)
 
-    fwd()
+    capi.gemm_fwd_repeat([fd], 1, s)
     path = capi.last_path()
     # timed region: exactly `steps` steps, synchronised on both sides
     for _ in range(warmup):
@@ -130,8 +146,8 @@ def headline(ctx, steps, warmup, dtype, M=4096, N=4096, K=4096, seed=3):
     e1.synchronize()
     wall = time.perf_counter() - t0
     step_ms = e0.elapsed_ms(e1) / steps
-    fwd_ms = ctx.time_ms(fwd, max(steps, 20))
-    bwd_ms = ctx.time_ms(bwd, max(steps, 20))
+    fwd_ms = ctx.time_repeat([fd], max(steps, 20), "fwd")
+    bwd_ms = ctx.time_repeat([bd], max(steps, 20), "bwd")
     flop = 2.0 * M * N * K
     return {
         "step_ms": step_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "wall_s": wall, "path": path,
@@ -156,19 +172,12 @@ def fp32_cfg(ctx, M, N, K, act, iters, seed):
     pX, pW, pb, pgY = ctx.put(X), ctx.put(W), ctx.put(b), ctx.put(gY)
     pY, pZ = ctx.empty(M * N * 4), ctx.empty(M * N * 4)
     pgA, pgB, pgb = ctx.empty(M * K * 4), ctx.empty(K * N * 4), ctx.empty(N * 4)
-    s = ctx.stream.ptr
-
-    def fwd():
-        capi.gemm_fwd(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
-                      bias_kind=capi.BIAS_PERN, act=act, stream=s)
-
-    def step():
-        fwd()
-        capi.gemm_bwd(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
-                      gBias=pgb, bias_kind=capi.BIAS_PERN, act=act, stream=s)
-
-    fwd_ms = ctx.time_ms(fwd, iters)
-    step_ms = ctx.time_ms(step, iters)
+    fd = capi.fwd_desc(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, Y=pY, Z=pZ, bias=pb,
+                       bias_kind=capi.BIAS_PERN, act=act)
+    bd = capi.bwd_desc(dtype=capi.F32, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
+                       gBias=pgb, bias_kind=capi.BIAS_PERN, act=act)
+    fwd_ms = ctx.time_repeat([fd], iters, "fwd")
+    step_ms = fwd_ms + ctx.time_repeat([bd], iters, "bwd")
     flop = 2.0 * M * N * K
     return {"fwd_us": fwd_ms * 1e3, "step_us": step_ms * 1e3,
             "tflops_fwd": flop / (fwd_ms * 1e-3) / 1e12,
@@ -192,23 +201,14 @@ def sdpa_cfg(ctx, dtype, iters, sets=8):
         P /= P.sum(-1, keepdims=True)
         bufs.append((ctx.put(Q), ctx.put(Kt), ctx.put(V), ctx.put(capi.to_storage(P, dtype)),
                      ctx.empty(BH * L * L * es), ctx.empty(BH * L * D * es)))
-    s = ctx.stream.ptr
-    it = [0]
-
-    def qk():
-        q, k, _, _, S, _ = bufs[it[0] % sets]
-        it[0] += 1
-        capi.gemm_fwd(dtype=dtype, M=L, N=L, K=D, A=q, B=k, Y=S, trans_b=True, alpha=0.125,
-                      batch=BH, stride_a=L * D, stride_b=L * D, stride_y=L * L, stream=s)
-
-    def pv():
-        _, _, v, p, _, y = bufs[it[0] % sets]
-        it[0] += 1
-        capi.gemm_fwd(dtype=dtype, M=L, N=D, K=L, A=p, B=v, Y=y, batch=BH,
-                      stride_a=L * L, stride_b=L * D, stride_y=L * D, stream=s)
-
-    qk_ms = ctx.time_ms(qk, iters)
-    pv_ms = ctx.time_ms(pv, iters)
+    qk = [capi.fwd_desc(dtype=dtype, M=L, N=L, K=D, A=q, B=k, Y=S, trans_b=True, alpha=0.125,
+                        batch=BH, stride_a=L * D, stride_b=L * D, stride_y=L * L)
+          for q, k, _, _, S, _ in bufs]
+    pv = [capi.fwd_desc(dtype=dtype, M=L, N=D, K=L, A=p, B=v, Y=y, batch=BH,
+                        stride_a=L * L, stride_b=L * D, stride_y=L * D)
+          for _, _, v, p, _, y in bufs]
+    qk_ms = ctx.time_repeat(qk, iters, "fwd")
+    pv_ms = ctx.time_repeat(pv, iters, "fwd")
     flop = 2.0 * BH * L * L * D
     byt_qk = (2 * BH * L * D + BH * L * L) * es
     byt_pv = (BH * L * L + 2 * BH * L * D) * es
@@ -230,13 +230,9 @@ def conv_cfg(ctx, dtype, iters):
     b = normal(g, (N,), 0.02)
     pA, pW, pb = ctx.put(col), ctx.put(W), ctx.put(b)
     pY, pZ = ctx.empty(M * N * es), ctx.empty(M * N * es)
-    s = ctx.stream.ptr
-
-    def fwd():
-        capi.gemm_fwd(dtype=dtype, M=M, N=N, K=K, A=pA, B=pW, Y=pY, Z=pZ, bias=pb,
-                      bias_kind=capi.BIAS_PERN, act="relu", stream=s)
-
-    ms = ctx.time_ms(fwd, iters)
+    fd = capi.fwd_desc(dtype=dtype, M=M, N=N, K=K, A=pA, B=pW, Y=pY, Z=pZ, bias=pb,
+                       bias_kind=capi.BIAS_PERN, act="relu")
+    ms = ctx.time_repeat([fd], iters, "fwd")
     flop = 2.0 * M * N * K
     byt = (M * K + K * N + 2 * M * N) * es + N * 4
     peak = PEAK_F32 if dtype == capi.F32 else PEAK_BF16
@@ -255,18 +251,11 @@ def skinny_cfg(ctx, iters, sets=10):
     pb = ctx.put(normal(g, (N,), 0.02))
     Ws = [ctx.put(capi.to_storage(normal(g, (K, N), 1 / np.sqrt(K)), capi.BF16)) for _ in range(sets)]
     pY = ctx.empty(M * N * 2)
-    s = ctx.stream.ptr
-    it = [0]
-
-    def fwd():
-        w = Ws[it[0] % sets]
-        it[0] += 1
-        capi.gemm_fwd(dtype=capi.BF16, M=M, N=N, K=K, A=pX, B=w, Y=pY, bias=pb,
-                      bias_kind=capi.BIAS_PERN, act="none", stream=s)
-
-    fwd()
+    fds = [capi.fwd_desc(dtype=capi.BF16, M=M, N=N, K=K, A=pX, B=w, Y=pY, bias=pb,
+                         bias_kind=capi.BIAS_PERN, act="none") for w in Ws]
+    capi.gemm_fwd_repeat(fds, 1, ctx.stream.ptr)
     path = capi.last_path()
-    ms = ctx.time_ms(fwd, iters)
+    ms = ctx.time_repeat(fds, iters, "fwd")
     byt = (M * K + K * N + M * N) * 2 + N * 4
     return {"fwd_us": ms * 1e3, "gbps": byt / (ms * 1e-3) / 1e9,
             "frac_hbm": byt / (ms * 1e-3) / 1e9 / PEAK_HBM, "path": path}
@@ -314,6 +303,12 @@ def main():
         raise SystemExit("no HIP device visible")
     name, cus, clk = capi.device_info(0)
     ctx = Ctx(capi)
+    if args.calib_copy:
+        nb = 256 << 20
+        src, dst = ctx.empty(nb), ctx.empty(nb)
+        capi.check(capi.lib().gev2_memcpy_dtod_async(dst, src, nb, ctx.stream.ptr), "calib copy")
+        ctx.stream.synchronize()
+        ctx.free()
     res = headline(ctx, args.steps, args.warmup, capi.BF16)
     print(f"# headline bf16 4096^3: step {res['step_ms']:.3f} ms, fwd {res['fwd_ms'] * 1e3:.1f} us "
           f"({res['tflops_fwd']:.0f} TFLOP/s), bwd {res['bwd_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)

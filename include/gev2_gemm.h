@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define GEV2_ABI_VERSION 1
+#define GEV2_ABI_VERSION 2
 
 /* Status (values of ai::cuda::shim::Status, ai_status.hpp:14-43) */
 enum {
@@ -102,6 +102,9 @@ typedef struct gev2_gemm_fwd_desc {
  *   gBias = sum of gZ over rows (PER_N, [N]) / columns (PER_M, [M]) / all (SCALAR)
  * Replaces GemmCudaBackward (launcher.cu:279-383 + regemm_backward.cu:151-301).
  * gBias is overwritten (the reference zero-fills it first, :190-197).
+ * For act none / ReLU / LeakyReLU, gZ is formed while the GEMM kernels load
+ * their operands and never stored; for the other activations it is written
+ * once to `workspace` and the two GEMMs read it.
  */
 typedef struct gev2_gemm_bwd_desc {
   int32_t dtype;
@@ -119,10 +122,25 @@ typedef struct gev2_gemm_bwd_desc {
   void* gB;       int64_t ldgb, stride_gb;
   void* gC;       int64_t ldgc, stride_gc;
   float* gBias;   int64_t stride_gbias;
+  /* Optional scratch for dY' = dY (.) act'(Z) in dtype, batch*M*N elements,
+   * used for GELU / Sigmoid / Tanh (whose act' is not fused into the GEMM
+   * operand loads).  NULL or too small: the library uses a buffer it allocates
+   * once per (device, stream) and keeps (make that first call outside HIP-graph
+   * capture).  Plays the role of the reference's GemmWorkspace::scratch
+   * (gemm/api.hpp:97-104). */
+  void* workspace; int64_t workspace_bytes;
 } gev2_gemm_bwd_desc;
 
 int gev2_gemm_fwd(const gev2_gemm_fwd_desc* desc, void* stream);
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
+
+/*
+ * Benchmark helpers (no counterpart in the reference): issue `reps` calls back
+ * to back on `stream`, call i using descs[i % n_descs] (rotating buffer sets),
+ * so that a timing of small problems measures the device, not the caller.
+ */
+int gev2_gemm_fwd_repeat(const gev2_gemm_fwd_desc* descs, int n_descs, int reps, void* stream);
+int gev2_gemm_bwd_repeat(const gev2_gemm_bwd_desc* descs, int n_descs, int reps, void* stream);
 
 int gev2_abi_version(void);
 const char* gev2_status_string(int status);
