@@ -16,8 +16,6 @@
 #include "gev2_kernels.hpp"
 
 namespace gev2 {
-int skinny_slab_cols(int dtype);
-int skinny_max_ks();
 
 hipError_t launch_tile(int dtype, int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
                        int batch, hipStream_t s) {
@@ -125,48 +123,7 @@ const char* cfg_name(int cfg, bool vec) {
   }
 }
 
-// Split-K workspace of the skinny kernel: one per (device, stream) so that
-// streams do not share partial sums.  Counters start at zero and every launch
-// leaves them at zero.
-struct SkinnyWs {
-  float* partial = nullptr;
-  size_t partial_bytes = 0;
-  unsigned* counters = nullptr;
-  size_t counter_count = 0;
-};
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, SkinnyWs> g_ws;
-
-int get_skinny_ws(hipStream_t s, size_t partial_bytes, size_t counters, SkinnyWs** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  SkinnyWs& ws = g_ws[{dev, s}];
-  if (ws.partial_bytes < partial_bytes) {
-    if (ws.partial) (void)hipFree(ws.partial);
-    ws.partial = nullptr;
-    ws.partial_bytes = 0;
-    e = hipMalloc(&ws.partial, partial_bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(skinny partials)");
-    ws.partial_bytes = partial_bytes;
-  }
-  if (ws.counter_count < counters) {
-    // the previous counters may still be in use by queued work on this stream
-    e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    if (ws.counters) (void)hipFree(ws.counters);
-    ws.counters = nullptr;
-    ws.counter_count = 0;
-    e = hipMalloc(&ws.counters, counters * sizeof(unsigned));
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(skinny counters)");
-    e = hipMemset(ws.counters, 0, counters * sizeof(unsigned));
-    if (e != hipSuccess) return hip_fail(e, "hipMemset(skinny counters)");
-    ws.counter_count = counters;
-  }
-  *out = &ws;
-  return GEV2_OK;
-}
 
 // dY' workspace of the backward for non-linear activations, one per
 // (device, stream), grown on demand.  hipFree waits for queued work that may
@@ -257,29 +214,15 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
                          N % epc == 0 && vec_ok(d->B, ldb, 0, N, K, 1, d->dtype) &&
                          env_int("GEV2_NO_SKINNY", 0) == 0;
   if (skinny_ok) {
-    const int slab = gev2::skinny_slab_cols(d->dtype);
-    const int64_t slabs = (N + slab - 1) / slab;
-    // splits: enough workgroups for 2 per CU, each split a multiple of the
-    // kernel's 128-row loop step
-    int64_t splits = std::max<int64_t>(1, (512 + slabs - 1) / slabs);
-    int64_t kps = (K + splits - 1) / splits;
-    kps = ((kps + 127) / 128) * 128;
-    if (kps > gev2::skinny_max_ks()) kps = gev2::skinny_max_ks();
-    splits = (K + kps - 1) / kps;
-    SkinnyWs* ws = nullptr;
-    st = get_skinny_ws(s, static_cast<size_t>(splits * M * N) * sizeof(float),
-                       static_cast<size_t>(slabs), &ws);
-    if (st != GEV2_OK) return st;
     gev2::SkinnyArgs a{};
     a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z;
     a.bias = has_bias ? d->bias : nullptr;
-    a.partial = ws->partial; a.counters = ws->counters;
     a.lda = lda; a.ldb = ldb; a.ldd = ldy; a.ldzo = ldz;
     a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
     a.act = d->act; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
     a.slope = d->leaky_slope; a.alpha = d->alpha;
-    a.k_per_split = static_cast<int>(kps); a.splits = static_cast<int>(splits);
-    hipError_t e = gev2::launch_skinny(d->dtype, a, slab, s);
+    a.x_vec = (aligned16(d->A) && lda % epc == 0 && K % epc == 0) ? 1 : 0;
+    hipError_t e = gev2::launch_skinny(d->dtype, a, s);
     if (e != hipSuccess) return hip_fail(e, "skinny launch");
     t_last_path = "skinny";
     return GEV2_OK;
@@ -337,29 +280,62 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
   const bool scalar_loads = env_int("GEV2_SCALAR_LOADS", 0) != 0;
 
-  // dY' operand of the two GEMMs: gY with act'(Z) applied while loading
-  // (piecewise-linear activations), or gZ materialised once in a workspace.
+  // dY' operand of the two GEMMs: gY with act'(Z) applied while the GEMM
+  // kernels load it (piecewise-linear activations on small problems), or gZ
+  // materialised once in a workspace.  Materialising costs one pass over
+  // dY/Z (and yields dBias), but lets both GEMMs use the plain 256x256 kernels;
+  // the transcendental activations always take it, so that their act' is
+  // evaluated once per element rather than once per workgroup loading it.
   const bool linear = d->act == GEV2_ACT_NONE || d->act == GEV2_ACT_RELU || d->act == GEV2_ACT_LEAKY_RELU;
+  const double work = static_cast<double>(M) * N * K * batch;
   const void* G = d->gY;
   int64_t ldG = ldgy, sG = d->stride_gy;
   bool fused = true;
-  if (!linear && (d->gA || d->gB)) {
-    const int64_t need = static_cast<int64_t>(batch) * M * N * es;
+  bool bias_done = false;
+  if ((!linear || work >= (1u << 30)) && (d->gA || d->gB) && env_int("GEV2_FUSED_BWD", 0) == 0) {
+    const int epc = elems_per_chunk(dt);
+    const bool prep_vec = !scalar_loads && N % epc == 0 && vec_ok(d->gY, ldgy, d->stride_gy, N, M, batch, dt) &&
+                          vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt);
+    const bool sums = prep_vec && want_bias && d->bias_kind == GEV2_BIAS_PER_N;
+    const int row_blocks = static_cast<int>((M + gev2::kPrepRows - 1) / gev2::kPrepRows);
+    const int64_t gz_bytes = ((static_cast<int64_t>(batch) * M * N * es + 255) / 256) * 256;
+    const int64_t part_bytes = sums ? static_cast<int64_t>(batch) * row_blocks * N * 4 : 0;
+    const int64_t need = gz_bytes + part_bytes;
     void* ws = nullptr;
-    if (d->workspace && d->workspace_bytes >= need && aligned16(d->workspace)) {
+    if (d->workspace && d->workspace_bytes >= need && (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
       ws = d->workspace;
     } else {
       st = get_grad_ws(s, static_cast<size_t>(need), &ws);
       if (st != GEV2_OK) return st;
     }
-    gev2::GradArgs g{};
-    g.gY = d->gY; g.Z = d->Z; g.out = ws; g.gbias = nullptr;
-    g.ldgy = ldgy; g.ldz = ldz; g.ldout = N;
-    g.sgY = d->stride_gy; g.sZ = d->stride_z; g.sOut = M * N; g.sGbias = 0;
-    g.M = static_cast<int>(M); g.N = static_cast<int>(N);
-    g.act = d->act; g.slope = d->leaky_slope; g.beta = 1.0f; g.bias_kind = GEV2_BIAS_NONE;
-    hipError_t e = gev2::launch_grad_elementwise(dt, g, batch, s);
-    if (e != hipSuccess) return hip_fail(e, "gZ launch");
+    float* partial = sums ? reinterpret_cast<float*>(static_cast<char*>(ws) + gz_bytes) : nullptr;
+    hipError_t e;
+    if (prep_vec) {
+      gev2::PrepArgs pa{};
+      pa.gY = d->gY; pa.Z = d->Z; pa.out = ws; pa.partial = partial;
+      pa.ldgy = ldgy; pa.ldz = ldz;
+      pa.sgY = d->stride_gy; pa.sZ = d->stride_z; pa.sOut = M * N;
+      pa.sPartial = static_cast<int64_t>(row_blocks) * N;
+      pa.M = static_cast<int>(M); pa.N = static_cast<int>(N);
+      pa.act = d->act; pa.slope = d->leaky_slope;
+      e = gev2::launch_grad_prep(dt, pa, batch, s);
+      if (e != hipSuccess) return hip_fail(e, "gZ launch");
+      if (sums) {
+        e = gev2::launch_finish_col_sums(partial, pa.sPartial, row_blocks, static_cast<int>(N), d->gBias,
+                                         d->stride_gbias, batch, s);
+        if (e != hipSuccess) return hip_fail(e, "dBias launch");
+        bias_done = true;
+      }
+    } else {
+      gev2::GradArgs g{};
+      g.gY = d->gY; g.Z = d->Z; g.out = ws; g.gbias = nullptr;
+      g.ldgy = ldgy; g.ldz = ldz; g.ldout = N;
+      g.sgY = d->stride_gy; g.sZ = d->stride_z; g.sOut = M * N; g.sGbias = 0;
+      g.M = static_cast<int>(M); g.N = static_cast<int>(N);
+      g.act = d->act; g.slope = d->leaky_slope; g.beta = 1.0f; g.bias_kind = GEV2_BIAS_NONE;
+      e = gev2::launch_grad_elementwise(dt, g, batch, s);
+      if (e != hipSuccess) return hip_fail(e, "gZ launch");
+    }
     G = ws; ldG = N; sG = M * N;
     fused = false;
   }
@@ -406,7 +382,7 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     hipError_t e = gev2::launch_tile(dt, cfg, true, false, fused ? 2 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dW launch");
   }
-  if (d->gC || (want_bias && !fuse_bias)) {
+  if (d->gC || (want_bias && !fuse_bias && !bias_done)) {
     gev2::GradArgs g{};
     g.gY = d->gY; g.Z = d->Z; g.out = d->gC; g.gbias = d->gBias;
     g.ldgy = ldgy; g.ldz = ldz; g.ldout = ldgc;
@@ -417,7 +393,7 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       hipError_t e = gev2::launch_grad_elementwise(dt, g, batch, s);
       if (e != hipSuccess) return hip_fail(e, "gC launch");
     }
-    if (want_bias && !fuse_bias) {
+    if (want_bias && !fuse_bias && !bias_done) {
       hipError_t e = gev2::launch_bias_grad(dt, g, batch, s);
       if (e != hipSuccess) return hip_fail(e, "bias-grad launch");
     }
@@ -509,16 +485,6 @@ int gev2_stream_create(void** stream) {
 int gev2_stream_destroy(void* stream) {
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (auto it = g_ws.begin(); it != g_ws.end();) {
-      if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
-        (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
-        if (it->second.partial) (void)hipFree(it->second.partial);
-        if (it->second.counters) (void)hipFree(it->second.counters);
-        it = g_ws.erase(it);
-      } else {
-        ++it;
-      }
-    }
     for (auto it = g_grad_ws.begin(); it != g_grad_ws.end();) {
       if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
         (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));

@@ -93,6 +93,101 @@ __global__ void __launch_bounds__(256) bias_grad_all_kernel(GradArgs p) {
   if (threadIdx.x == 0) p.gbias[(int64_t)bz * p.sGbias] = red[0] + red[1] + red[2] + red[3];
 }
 
+// grad_prep: 256 threads = 32 chunk columns x 8 row lanes; a workgroup covers
+// kPrepRows rows x (32 * EPC) columns.  Each thread walks its rows in order,
+// the 8 row lanes are then added in order: the partial sums are deterministic.
+template <typename T>
+__global__ void __launch_bounds__(256) grad_prep_kernel(PrepArgs p) {
+  constexpr int EPC = Elem<T>::kPerChunk;
+  constexpr int COLS = 32 * EPC;
+  __shared__ float red[8][COLS];
+  const int bz = blockIdx.z;
+  const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
+  const T* Z = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ;
+  T* out = reinterpret_cast<T*>(p.out) + (int64_t)bz * p.sOut;
+  const int cc = threadIdx.x & 31, rl = threadIdx.x >> 5;
+  const int n = blockIdx.x * COLS + cc * EPC;
+  const int r0 = blockIdx.y * kPrepRows;
+  const bool nok = n < p.N;
+  float sum[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) sum[e] = 0.f;
+  dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+#pragma unroll 4
+    for (int r = rl; r < kPrepRows; r += 8) {
+      const int m = r0 + r;
+      if (!nok || m >= p.M) continue;
+      const u32x4 g = *reinterpret_cast<const u32x4*>(gY + (int64_t)m * p.ldgy + n);
+      const u32x4 z = *reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n);
+      float gv[EPC], zv[EPC];
+      chunk_to_f32<T>(g, gv);
+      chunk_to_f32<T>(z, zv);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        gv[e] *= act_grad_t<ACT>(zv[e], p.slope);
+        sum[e] += gv[e];
+      }
+      *reinterpret_cast<u32x4*>(out + (int64_t)m * p.N + n) = f32_to_chunk<T>(gv);
+    }
+  });
+  if (!p.partial) return;
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) red[rl][cc * EPC + e] = sum[e];
+  __syncthreads();
+  const int c = threadIdx.x;
+  if (c < COLS && blockIdx.x * COLS + c < p.N) {
+    float s = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s += red[l][c];
+    p.partial[(int64_t)bz * p.sPartial + (int64_t)blockIdx.y * p.N + blockIdx.x * COLS + c] = s;
+  }
+}
+
+// 64 columns x 4 row-block lanes per workgroup: lane g adds row blocks
+// g, g+4, ... in order (independent loads, unrolled), then the 4 lanes are
+// added in order.
+__global__ void __launch_bounds__(256) finish_col_sums_kernel(const float* partial, int64_t sPartial,
+                                                              int row_blocks, int N, float* gbias,
+                                                              int64_t sGbias) {
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + c;
+  const int bz = blockIdx.y;
+  float s = 0.f;
+  if (n < N) {
+    const float* pp = partial + (int64_t)bz * sPartial + n;
+#pragma unroll 8
+    for (int rb = g; rb < row_blocks; rb += 4) s += pp[(int64_t)rb * N];
+  }
+  red[g][c] = s;
+  __syncthreads();
+  if (g == 0 && n < N) gbias[(int64_t)bz * sGbias + n] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+}
+
+template <typename T>
+static hipError_t grad_prep_t(const PrepArgs& a, int batch, hipStream_t s) {
+  constexpr int COLS = 32 * Elem<T>::kPerChunk;
+  dim3 grid((a.N + COLS - 1) / COLS, (a.M + kPrepRows - 1) / kPrepRows, batch);
+  hipLaunchKernelGGL(grad_prep_kernel<T>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_grad_prep(int dtype, const PrepArgs& a, int batch, hipStream_t s) {
+  switch (dtype) {
+    case kF32: return grad_prep_t<float>(a, batch, s);
+    case kBF16: return grad_prep_t<__bf16>(a, batch, s);
+    case kF16: return grad_prep_t<_Float16>(a, batch, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
+                                  float* gbias, int64_t sGbias, int batch, hipStream_t s) {
+  hipLaunchKernelGGL(finish_col_sums_kernel, dim3((N + 63) / 64, batch), dim3(256), 0, s, partial, sPartial,
+                     row_blocks, N, gbias, sGbias);
+  return hipGetLastError();
+}
+
 template <typename T>
 static hipError_t grad_elementwise_t(const GradArgs& a, int batch, hipStream_t s) {
   const int64_t total = (int64_t)a.M * a.N;

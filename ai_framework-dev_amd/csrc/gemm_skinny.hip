@@ -1,18 +1,21 @@
 // Bandwidth-bound forward for skinny shapes, Y[M,N] = act(alpha * X[M,K] W[K,N] + b)
-// with M <= 16 (the reference runs these through its 128x128 FFMA tile and
-// leaves almost every workgroup idle: regemm_gemm_bias_act.cu:254-395 with a
+// with M <= 16.  The reference runs these through its 128x128 FFMA tile and
+// leaves almost every workgroup idle (regemm_gemm_bias_act.cu:254-395 with a
 // (N/128, 1) grid).
 //
-// W dominates the traffic (K*N elements, read exactly once).  The grid is
-// (N / slab) x splits: each workgroup streams a [K/splits, slab] block of W
-// with 16-byte loads (16 lanes cover one slab row, 16 row groups per
-// workgroup), keeps its slice of X in LDS, and accumulates M x (8 or 4)
-// fp32 sums per lane -- v_dot2_f32_{bf16,f16} on row pairs for 16-bit data,
-// FMA for fp32.  Row-group sums are reduced in LDS and written as one fp32
-// partial per (split, m, n).  The last workgroup of a slab to arrive (an
-// arrival counter per slab) adds the partials in split order, applies
-// bias/activation/Z and stores Y, then resets the counter: deterministic and
-// single-launch.
+// W dominates the traffic (K*N elements, read exactly once), so the kernel is
+// built around streaming it:
+//   - one workgroup per slab of 32 bytes of every W row (16 bf16/f16 columns or
+//     8 fp32 columns), covering all of K: no cross-workgroup reduction, hence
+//     no device-scope fence (which on an 8-XCD part writes back L2);
+//   - slabs are assigned so that the workgroups of one XCD take adjacent slabs
+//     and share each 128-byte line of W through that XCD's L2;
+//   - each lane pair reads one row's 32 bytes with 16-byte loads, a thread's
+//     rows of a K chunk are all in flight at once;
+//   - X[:, chunk] sits in LDS as k-pairs (x[k][m], x[k+1][m]), so 16-bit data
+//     uses v_dot2_f32_{bf16,f16} on W row pairs; fp32 uses FMA;
+//   - the 128 row lanes are summed by a fixed shuffle tree and a fixed-order
+//     LDS pass (deterministic), then bias / activation / Z / Y.
 #include "gev2_device.hpp"
 #include "gev2_kernels.hpp"
 
@@ -32,176 +35,169 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   }
 }
 
-constexpr int kSkLanesPerRow = 16;  // lanes covering one slab row
-constexpr int kSkRowGroups = 16;    // 256 threads
-constexpr int kSkThreads = kSkLanesPerRow * kSkRowGroups;
-static_assert(kSkLanesPerRow * 8 <= kSkThreads, "one thread per slab column in the reduction");
-constexpr int kSkMaxKs = 1024;      // max K rows per split (LDS X slice)
-constexpr int kSkStep = 128;        // K rows per main-loop iteration (both variants)
+constexpr int kOobOffsetSk = static_cast<int>(0x80000000u);
+constexpr int kSkThreads = 256;
+constexpr int kSkRowLanes = kSkThreads / 2;   // lane pairs
 
-// Slab width in columns: 16 lanes x one 16-byte chunk each.
-template <typename T> constexpr int slab_cols() { return kSkLanesPerRow * Elem<T>::kPerChunk; }
+template <typename T> constexpr int sk_cols() { return 2 * Elem<T>::kPerChunk; }
+
+// K rows per LDS chunk of X: the whole of K = 4096 for 16-bit data with
+// M <= 8, so that a thread has all of its W rows in flight at once.
+template <typename T, int MAXM>
+constexpr int sk_chunk() { return (sizeof(T) == 2 && MAXM == 8) ? 4096 : 2048; }
 
 template <typename T, int MAXM>
 __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(SkinnyArgs p) {
-  constexpr int EPC = Elem<T>::kPerChunk;
-  constexpr int NS = slab_cols<T>();
+  constexpr int kSkChunk = sk_chunk<T, MAXM>();
   constexpr bool kHalf = sizeof(T) == 2;
-  // X slice: for 16-bit, dword (x[m][k], x[m][k+1]) pairs; for fp32, floats.
-  __shared__ uint32_t xs[MAXM * kSkMaxKs / (kHalf ? 2 : 1)];
-  __shared__ float red[kSkRowGroups][NS];
-  __shared__ unsigned last_flag;
+  constexpr int EPC = Elem<T>::kPerChunk;
+  constexpr int COLS = sk_cols<T>();
+  // rows each thread handles per chunk: 16-bit data in k pairs
+  constexpr int RSTEP = kHalf ? 2 : 1;
+  constexpr int RPT = kSkChunk / (kSkRowLanes * RSTEP);
+  // X chunk: 16-bit -> dwords (x[k][m], x[k+1][m]) at [k/2][m]; fp32 -> [k][m]
+  // X chunk, reused for the final reduction (MH * EPC * 256 floats)
+  constexpr int MH = MAXM < 8 ? MAXM : 8;
+  constexpr int XS = (kSkChunk / RSTEP) * MAXM, RS = MH * EPC * kSkThreads;
+  __shared__ uint32_t xs[XS > RS ? XS : RS];
 
   const int tid = threadIdx.x;
-  const int ln = tid % kSkLanesPerRow, rg = tid / kSkLanesPerRow;
-  const int slab = blockIdx.x, split = blockIdx.y;
-  const int n0 = slab * NS;
-  const int ncol = n0 + ln * EPC;
-  const int kbeg = split * p.k_per_split;
-  const int kend = min(p.K, kbeg + p.k_per_split);
+  const int h = tid & 1, rl = tid >> 1;
+  // XCD-aware slab order: workgroup i runs on XCD i % 8
+  int slab = blockIdx.x;
+  const int nslab = gridDim.x;
+  if ((nslab & 7) == 0) slab = (slab & 7) * (nslab >> 3) + (slab >> 3);
+  const int n = slab * COLS + h * EPC;
+  const bool nok = n < p.N;   // N % EPC == 0 (host)
   const int M = p.M;
 
   const T* X = reinterpret_cast<const T*>(p.A);
-  const T* W = reinterpret_cast<const T*>(p.B);
-
-  // stage X[:, kbeg:kbeg+ks) into LDS, zero beyond kend; ks is padded to the
-  // main loop's full step (128 rows) so that every LDS entry the loop reads was
-  // written in this launch
-  {
-    const int ks = (p.k_per_split + kSkStep - 1) / kSkStep * kSkStep;
-    if constexpr (kHalf) {
-      const int pairs = ks / 2;
-      for (int idx = tid; idx < MAXM * pairs; idx += kSkThreads) {
-        const int m = idx / pairs, j = idx - m * pairs;
-        const int k = kbeg + 2 * j;
-        uint32_t lo = 0, hi = 0;
-        if (m < M && k < kend) lo = *reinterpret_cast<const uint16_t*>(X + (int64_t)m * p.lda + k);
-        if (m < M && k + 1 < kend) hi = *reinterpret_cast<const uint16_t*>(X + (int64_t)m * p.lda + k + 1);
-        xs[m * (kSkMaxKs / 2) + j] = lo | (hi << 16);
-      }
-    } else {
-      for (int idx = tid; idx < MAXM * ks; idx += kSkThreads) {
-        const int m = idx / ks, j = idx - m * ks;
-        const int k = kbeg + j;
-        xs[m * kSkMaxKs + j] = (m < M && k < kend) ? __float_as_uint(X[(int64_t)m * p.lda + k]) : 0u;
-      }
-    }
-  }
-  __syncthreads();
-
+  const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), static_cast<short>(0),
+                                                                      0x7fffffff, 0x00020000);
   float acc[MAXM][EPC];
 #pragma unroll
   for (int m = 0; m < MAXM; ++m)
 #pragma unroll
-    for (int c = 0; c < EPC; ++c) acc[m][c] = 0.f;
+    for (int e = 0; e < EPC; ++e) acc[m][e] = 0.f;
 
-  const bool col_ok = ncol < p.N;   // N % EPC == 0 is required by the host
-  const T* wcol = W + ncol;
-  if constexpr (kHalf) {
-    // rows kbeg + 2*rg + 32*i (+1)
-    constexpr int U = 4;
-    static_assert(2 * kSkRowGroups * U == kSkStep, "loop step");
-    for (int kb = kbeg + 2 * rg; kb < kend; kb += 2 * kSkRowGroups * U) {
-      u32x4 w0[U], w1[U];
+  for (int kc0 = 0; kc0 < p.K; kc0 += kSkChunk) {
+    // W rows of this thread: k = kc0 + (rl + kSkRowLanes * i) * RSTEP (+1)
+    u32x4 w[RPT][RSTEP];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = kb + u * 2 * kSkRowGroups;
-        const bool ok0 = col_ok && k < kend, ok1 = col_ok && k + 1 < kend;
-        w0[u] = ok0 ? *reinterpret_cast<const u32x4*>(wcol + (int64_t)k * p.ldb) : u32x4{0, 0, 0, 0};
-        w1[u] = ok1 ? *reinterpret_cast<const u32x4*>(wcol + (int64_t)(k + 1) * p.ldb) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int r = 0; r < RSTEP; ++r) {
+        const int k = kc0 + (rl + kSkRowLanes * i) * RSTEP + r;
+        const int off = (nok && k < p.K) ? static_cast<int>(((int64_t)k * p.ldb + n) * sizeof(T)) : kOobOffsetSk;
+        w[i][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off, 0, 0));
       }
+    // stage X[:, kc0 : kc0 + kSkChunk) (zero beyond M and K); with x_vec each
+    // thread reads 16 bytes (EPC consecutive k of one row m)
+    __syncthreads();
+    if (p.x_vec) {
+      for (int idx = tid; idx < (kSkChunk / EPC) * MAXM; idx += kSkThreads) {
+        const int m = idx % MAXM, j = idx / MAXM;
+        const int k = kc0 + j * EPC;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (m < M && k < p.K) v = *reinterpret_cast<const u32x4*>(X + (int64_t)m * p.lda + k);
+        if constexpr (kHalf) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = kb + u * 2 * kSkRowGroups;
-        const int j = (k - kbeg) >> 1;
+          for (int q = 0; q < 4; ++q) xs[(4 * j + q) * MAXM + m] = v[q];   // (x[k+2q], x[k+2q+1])
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xs[(4 * j + q) * MAXM + m] = v[q];
+        }
+      }
+    } else if constexpr (kHalf) {
+      for (int idx = tid; idx < (kSkChunk / 2) * MAXM; idx += kSkThreads) {
+        const int m = idx % MAXM, j = idx / MAXM;
+        const int k = kc0 + 2 * j;
+        uint32_t lo = 0, hi = 0;
+        if (m < M && k < p.K) lo = *reinterpret_cast<const uint16_t*>(X + (int64_t)m * p.lda + k);
+        if (m < M && k + 1 < p.K) hi = *reinterpret_cast<const uint16_t*>(X + (int64_t)m * p.lda + k + 1);
+        xs[j * MAXM + m] = lo | (hi << 16);
+      }
+    } else {
+      for (int idx = tid; idx < kSkChunk * MAXM; idx += kSkThreads) {
+        const int m = idx % MAXM, j = idx / MAXM;
+        const int k = kc0 + j;
+        xs[j * MAXM + m] = (m < M && k < p.K) ? __float_as_uint(X[(int64_t)m * p.lda + k]) : 0u;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int j = rl + kSkRowLanes * i;   // k pair (16-bit) or k (fp32) within the chunk
+      const u32x4* xv = reinterpret_cast<const u32x4*>(xs + j * MAXM);
+      if constexpr (kHalf) {
         uint32_t pr[8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          pr[2 * q] = (w0[u][q] & 0xffffu) | (w1[u][q] << 16);
-          pr[2 * q + 1] = (w0[u][q] >> 16) | (w1[u][q] & 0xffff0000u);
+          pr[2 * q] = (w[i][0][q] & 0xffffu) | (w[i][1][q] << 16);
+          pr[2 * q + 1] = (w[i][0][q] >> 16) | (w[i][1][q] & 0xffff0000u);
         }
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-          const uint32_t xm = xs[m * (kSkMaxKs / 2) + min(j, kSkMaxKs / 2 - 1)];
+        for (int mq = 0; mq < MAXM / 4; ++mq) {
+          const u32x4 x4 = xv[mq];
 #pragma unroll
-          for (int c = 0; c < 8; ++c) acc[m][c] = dot2<T>(pr[c], xm, acc[m][c]);
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[mq * 4 + t][e] = dot2<T>(pr[e], x4[t], acc[mq * 4 + t][e]);
         }
-      }
-    }
-  } else {
-    constexpr int U = 8;
-    static_assert(kSkRowGroups * U == kSkStep, "loop step");
-    for (int kb = kbeg + rg; kb < kend; kb += kSkRowGroups * U) {
-      u32x4 w[U];
+      } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int k = kb + u * kSkRowGroups;
-        w[u] = (col_ok && k < kend) ? *reinterpret_cast<const u32x4*>(wcol + (int64_t)k * p.ldb)
-                                    : u32x4{0, 0, 0, 0};
-      }
+        for (int mq = 0; mq < MAXM / 4; ++mq) {
+          const u32x4 x4 = xv[mq];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int j = min(kb + u * kSkRowGroups - kbeg, kSkMaxKs - 1);
+          for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-          const float xm = __uint_as_float(xs[m * kSkMaxKs + j]);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(xm, __uint_as_float(w[u][c]), acc[m][c]);
+            for (int e = 0; e < 4; ++e)
+              acc[mq * 4 + t][e] = fmaf(__uint_as_float(x4[t]), __uint_as_float(w[i][0][e]), acc[mq * 4 + t][e]);
         }
       }
     }
   }
 
-  // reduce the 16 row groups, one output row at a time
-  float* part = p.partial + (int64_t)split * M * p.N;
-#pragma unroll
-  for (int m = 0; m < MAXM; ++m) {
-    if (m < M) {   // uniform across the workgroup
-#pragma unroll
-      for (int c = 0; c < EPC; ++c) red[rg][ln * EPC + c] = acc[m][c];
-      __syncthreads();
-      if (tid < NS) {
-        float s = 0.f;
-#pragma unroll
-        for (int g = 0; g < kSkRowGroups; ++g) s += red[g][tid];
-        const int n = n0 + tid;
-        if (n < p.N) part[(int64_t)m * p.N + n] = s;
-      }
-      __syncthreads();
-    }
-  }
-
-  // arrival: the last workgroup of this slab finishes it
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[slab], 1u);
-    last_flag = (prev == static_cast<unsigned>(p.splits - 1)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-
+  // Sum over the 128 row lanes in a fixed order, MH rows of X at a time: each
+  // thread stores its sums at red[v][rl][h] (v = m * EPC + e), then two
+  // threads per output each add 64 row lanes in order and the pair is added.
+  float* red = reinterpret_cast<float*>(xs);
   T* Y = reinterpret_cast<T*>(p.D);
   T* Zo = reinterpret_cast<T*>(p.Zo);
-  for (int idx = tid; idx < M * NS; idx += kSkThreads) {
-    const int m = idx / NS, c = idx - m * NS;
-    const int n = n0 + c;
-    if (n >= p.N) continue;
+#pragma unroll
+  for (int m0 = 0; m0 < MAXM; m0 += MH) {
+    __syncthreads();
+#pragma unroll
+    for (int mm = 0; mm < MH; ++mm)
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) red[(mm * EPC + e) * kSkThreads + tid] = acc[m0 + mm][e];
+    __syncthreads();
+    // output o = (mm, c) for c < COLS; threads 2o, 2o+1
+    const int o = tid >> 1, part = tid & 1;
     float s = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) s += p.partial[((int64_t)sp * M + m) * p.N + n];
-    float pre = p.alpha == 1.f ? s : p.alpha * s;
-    if (p.bias) pre += load_bias(p.bias, p.bias_kind, m, n);
-    if (Zo) Elem<T>::store1(Zo + (int64_t)m * p.ldzo + n, pre);
-    Elem<T>::store1(Y + (int64_t)m * p.ldd + n, act_fwd(pre, p.act, p.slope));
+    const int mm = o / COLS, c = o % COLS;
+    if (mm < MH) {
+      const int hh = c / EPC, e = c % EPC;
+      const float* col = red + (mm * EPC + e) * kSkThreads + hh;
+      for (int r = part * 64; r < part * 64 + 64; ++r) s += col[2 * r];
+    }
+    const float s_hi = __shfl_xor(s, 1, 64);
+    const int m = m0 + mm;
+    const int nn = slab * COLS + c;
+    if (part == 0 && mm < MH && m < M && nn < p.N) {
+      const float tot = s + s_hi;
+      float pre = p.alpha == 1.f ? tot : p.alpha * tot;
+      if (p.bias) pre += load_bias(p.bias, p.bias_kind, m, nn);
+      if (Zo) Elem<T>::store1(Zo + (int64_t)m * p.ldzo + nn, pre);
+      Elem<T>::store1(Y + (int64_t)m * p.ldd + nn, act_fwd(pre, p.act, p.slope));
+    }
   }
-  if (tid == 0) p.counters[slab] = 0u;
 }
 
 template <typename T>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
-  constexpr int NS = slab_cols<T>();
-  dim3 grid((a.N + NS - 1) / NS, a.splits);
+  constexpr int COLS = sk_cols<T>();
+  dim3 grid((a.N + COLS - 1) / COLS);
   if (a.M <= 8)
     hipLaunchKernelGGL((gemm_skinny_kernel<T, 8>), grid, dim3(kSkThreads), 0, s, a);
   else
@@ -209,10 +205,7 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-int skinny_slab_cols(int dtype) { return dtype == kF32 ? slab_cols<float>() : slab_cols<__bf16>(); }
-int skinny_max_ks() { return kSkMaxKs; }
-
-hipError_t launch_skinny(int dtype, const SkinnyArgs& a, int, hipStream_t s) {
+hipError_t launch_skinny(int dtype, const SkinnyArgs& a, hipStream_t s) {
   switch (dtype) {
     case kF32: return launch_skinny_t<float>(a, s);
     case kBF16: return launch_skinny_t<__bf16>(a, s);

@@ -30,19 +30,17 @@ struct TileArgs {
   int store_vec;         // D/Zo rows allow 4-wide vector stores
 };
 
-// Skinny forward (M <= kSkinnyMaxM): split-K streaming over B with a
-// deterministic last-workgroup reduction of the fp32 partials.
+// Skinny forward (M <= kSkinnyMaxM): one workgroup per 32-byte column slab of
+// W over all of K (no cross-workgroup reduction, no workspace).
 constexpr int kSkinnyMaxM = 16;
 struct SkinnyArgs {
   const void* A; const void* B; void* D; void* Zo;
   const float* bias;
-  float* partial;        // [splits][M][N] fp32 workspace
-  unsigned* counters;    // [n_slabs] arrival counters, zero between launches
   int64_t lda, ldb, ldd, ldzo;
   int M, N, K;
   int act, bias_kind;
   float slope, alpha;
-  int k_per_split, splits;
+  int x_vec;             // X rows 16-byte aligned with K a multiple of the chunk
 };
 
 // Element-wise gZ = gY * act'(Z) (optionally scaled by beta) -> out, and
@@ -56,6 +54,22 @@ struct GradArgs {
   int act; float slope; float beta;
   int bias_kind;
 };
+
+// Vectorised dY' = dY (.) act'(Z) into a dense [M,N] buffer (16-byte chunks;
+// N a multiple of the chunk, rows 16-byte aligned) plus, when `partial` is
+// set, fixed-order column sums per block of kPrepRows rows: partial[rb][n].
+// finish_col_sums adds the row-block partials of each column in order.
+constexpr int kPrepRows = 64;
+struct PrepArgs {
+  const void* gY; const void* Z; void* out; float* partial;
+  int64_t ldgy, ldz;              // out has ld = N; partial has ld = N
+  int64_t sgY, sZ, sOut, sPartial;
+  int M, N;
+  int act; float slope;
+};
+hipError_t launch_grad_prep(int dtype, const PrepArgs& a, int batch, hipStream_t s);
+hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
+                                  float* gbias, int64_t sGbias, int batch, hipStream_t s);
 
 // Launcher entry points (each returns hipError_t from the launch).
 // Tile configuration ids, chosen by the host dispatcher.
@@ -74,7 +88,7 @@ hipError_t launch_tile_bf16(int cfg, bool ta, bool tb, int pro, bool vec, const 
                             int batch, hipStream_t s);
 hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
                            int batch, hipStream_t s);
-hipError_t launch_skinny(int dtype, const SkinnyArgs& a, int slab_cols, hipStream_t s);
+hipError_t launch_skinny(int dtype, const SkinnyArgs& a, hipStream_t s);
 hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const GradArgs& a, int batch, hipStream_t s);
 

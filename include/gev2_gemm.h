@@ -24,9 +24,9 @@
  *     GEV2_HIP_ERROR (130) is the reference's CUDA_ERROR slot.  The functions
  *     never throw; gev2_last_error() gives a message for the calling thread.
  *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = null stream).
- *   - gev2_gemm_fwd with 1 <= M <= 16 uses a split-K kernel whose partial sums
- *     live in a workspace the library allocates once per (device, stream) on
- *     first use: make that first call outside HIP-graph capture.
+ *   - gev2_gemm_fwd never allocates device memory.  gev2_gemm_bwd allocates
+ *     only when it materialises dY' and no large enough `workspace` is given
+ *     (see gev2_gemm_bwd_desc).
  */
 #ifndef GEV2_GEMM_H_
 #define GEV2_GEMM_H_
@@ -102,9 +102,9 @@ typedef struct gev2_gemm_fwd_desc {
  *   gBias = sum of gZ over rows (PER_N, [N]) / columns (PER_M, [M]) / all (SCALAR)
  * Replaces GemmCudaBackward (launcher.cu:279-383 + regemm_backward.cu:151-301).
  * gBias is overwritten (the reference zero-fills it first, :190-197).
- * For act none / ReLU / LeakyReLU, gZ is formed while the GEMM kernels load
- * their operands and never stored; for the other activations it is written
- * once to `workspace` and the two GEMMs read it.
+ * gZ is either formed while the GEMM kernels load their operands (act none /
+ * ReLU / LeakyReLU on problems below 2^30 multiply-adds) or written once to
+ * `workspace` by a pass that also sums dBias, after which the two GEMMs read it.
  */
 typedef struct gev2_gemm_bwd_desc {
   int32_t dtype;
@@ -122,12 +122,14 @@ typedef struct gev2_gemm_bwd_desc {
   void* gB;       int64_t ldgb, stride_gb;
   void* gC;       int64_t ldgc, stride_gc;
   float* gBias;   int64_t stride_gbias;
-  /* Optional scratch for dY' = dY (.) act'(Z) in dtype, batch*M*N elements,
-   * used for GELU / Sigmoid / Tanh (whose act' is not fused into the GEMM
-   * operand loads).  NULL or too small: the library uses a buffer it allocates
-   * once per (device, stream) and keeps (make that first call outside HIP-graph
-   * capture).  Plays the role of the reference's GemmWorkspace::scratch
-   * (gemm/api.hpp:97-104). */
+  /* Optional scratch (256-byte aligned) for dY' = dY (.) act'(Z): batch*M*N
+   * elements of dtype, rounded up to 256 bytes, plus batch*ceil(M/64)*N floats
+   * of dBias partial sums when a PerN gBias is requested.  Used when gZ is
+   * materialised: always for GELU / Sigmoid / Tanh, and for large problems
+   * (M*N*K*batch >= 2^30).  NULL or too small: the library uses a buffer it
+   * allocates once per (device, stream) and keeps (make that first call outside
+   * HIP-graph capture).  Plays the role of the reference's
+   * GemmWorkspace::scratch (gemm/api.hpp:97-104). */
   void* workspace; int64_t workspace_bytes;
 } gev2_gemm_bwd_desc;
 

@@ -295,13 +295,52 @@ def test_conv_im2col_form(gpu):
     del _check
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["materialised", "fused"])
+def test_backward_both_dy_paths(gpu, fused, monkeypatch):
+    """M*N*K = 2^30: the backward materialises dY' (vector pass + fixed-order dBias
+    partials) unless GEV2_FUSED_BWD forces the act'-prologue GEMMs; both must agree
+    with the oracle, and ReLU masks must agree bit for bit."""
+    capi = gpu
+    if fused:
+        monkeypatch.setenv("GEV2_FUSED_BWD", "1")
+    M = N = K = 1024
+    dtype = BF16
+    X, W, b = make_fwd_inputs(77, M, N, K, dtype, O.BIAS_PERN)
+    gY = rounded(np.random.default_rng(78).standard_normal((M, N)), dtype)
+    dev = Dev(capi)
+    try:
+        Y, Z, _ = run_fwd(capi, dev, X, W, b, O.BIAS_PERN, "relu", dtype)
+        pX, pW = dev.put(capi.to_storage(X, dtype)), dev.put(capi.to_storage(W, dtype))
+        pgY, pZ = dev.put(capi.to_storage(gY, dtype)), dev.put(capi.to_storage(Z, dtype))
+        pgA, pgB, pgb = dev.empty(M * K * 2), dev.empty(K * N * 2), dev.empty(N * 4)
+        capi.gemm_bwd(dtype=dtype, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, gA=pgA, gB=pgB,
+                      gBias=pgb, bias_kind=O.BIAS_PERN, act="relu")
+        capi.synchronize()
+        gA, gB = dev.get(pgA, (M, K), dtype), dev.get(pgB, (K, N), dtype)
+        gb = dev.get_f32(pgb, (N,))
+    finally:
+        dev.close()
+    ref = O.gemm_backward(X, W, gY, Z, "relu", bias_kind=O.BIAS_PERN)
+    aG, aY = np.abs(ref["gZ"]), np.abs(gY.astype(np.float64))
+    u = U_OUT[dtype]
+    Wt, Xt = np.abs(W.astype(np.float64)).T, np.abs(X.astype(np.float64)).T
+    assert_close(gA, ref["gA"], 1.01 * N * U_ACC * (aG @ Wt) + u * np.abs(ref["gA"]) + 1e-30, "gA",
+                 rel_norm=1e-2)
+    assert_close(gB, ref["gB"], 1.01 * M * U_ACC * (Xt @ aG) + u * np.abs(ref["gB"]) + 1e-30, "gB",
+                 rel_norm=1e-2)
+    assert_close(gb, ref["gBias"], 1.01 * M * U_ACC * aG.sum(0) + 1e-30, "gBias")
+
+
 def test_skinny_full_size(gpu):
     """BASELINE config 5b: M=8, N=K=4096, bf16, bias, through the skinny kernel."""
     path = _check_fwd(gpu, 8, 4096, 4096, BF16, "none", O.BIAS_PERN, seed=55)
     assert path == "skinny"
 
 
-def test_skinny_repeat_counters(gpu):
-    """The split-K arrival counters reset themselves: repeated calls stay correct."""
+def test_skinny_repeat_calls(gpu):
+    """Repeated skinny calls (X chunks staged per call in LDS) stay correct; K = 2048 + 640
+    also covers a partial second K chunk."""
     for i in range(3):
         _check_fwd(gpu, 4, 384, 2048, BF16, "relu", O.BIAS_PERN, seed=60 + i)
+    _check_fwd(gpu, 16, 264, 2688, F32, "gelu", O.BIAS_PERM, seed=64)
+    _check_fwd(gpu, 5, 136, 2688, F16, "none", O.BIAS_SCALAR, seed=65)
