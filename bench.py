@@ -261,8 +261,9 @@ def skinny_cfg(ctx, iters, sets=10):
             "frac_hbm": byt / (ms * 1e-3) / 1e9 / PEAK_HBM, "path": path}
 
 
-def cpu_baseline(M=4096, N=4096, K=4096, rows=512, reps=3):
-    """fp32 NumPy forward+backward (the reference's CPU path) on a row slice."""
+def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=40):
+    """fp32 NumPy forward+backward (the reference's CPU path) on the full C3 step,
+    repeated until about min_seconds of CPU work; the median step is reported."""
     from oracle import gemm_oracle as O
     try:
         from threadpoolctl import threadpool_info
@@ -271,24 +272,36 @@ def cpu_baseline(M=4096, N=4096, K=4096, rows=512, reps=3):
     except Exception:
         threads, blas = len(os.sched_getaffinity(0)), "?"
     g = np.random.default_rng(7)
-    X = normal(g, (rows, K), 1 / np.sqrt(K))
+    X = normal(g, (M, K), 1 / np.sqrt(K))
     W = normal(g, (K, N), 1 / np.sqrt(K))
     b = normal(g, (1, N), 0.02)
-    gY = normal(g, (rows, N))
+    gY = normal(g, (M, N))
     O.numpy_fp32_step(X, W, b, gY, "relu")   # warm-up
     ts = []
-    for _ in range(reps):
+    while len(ts) < max_reps and (len(ts) < 3 or sum(ts) < min_seconds):
         t0 = time.perf_counter()
         O.numpy_fp32_step(X, W, b, gY, "relu")
         ts.append(time.perf_counter() - t0)
     t = float(np.median(ts))
-    flop = 6.0 * rows * N * K
+    flop = 6.0 * M * N * K
     return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": int(threads),
             "kind": "port",
-            "sample": f"fp32 numpy fwd+bwd (np.matmul, {blas}) on a {rows}-row slice of the "
-                      f"4096^3 step ({rows}x{K} @ {K}x{N}), median of {reps}; "
-                      f"{t * 1e3:.1f} ms per slice, full step extrapolates to "
-                      f"{t * M / rows:.2f} s"}
+            "sample": f"fp32 numpy forward+backward (np.matmul via {blas}) of the full {M}x{K} @ "
+                      f"{K}x{N} ReLU step, {len(ts)} repetitions ({sum(ts):.1f} s of CPU work), "
+                      f"median {t * 1e3:.1f} ms per step"}
+
+
+def measured_traffic():
+    """HBM bytes per forward launch, as recorded from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (scaled by a copy of known size) in profiles/; None if absent."""
+    path = os.path.join(REPO, "profiles", "gemm_pipe_bf16_256x256_nn_4096_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -355,8 +368,8 @@ def main():
                                "Z saved; step = forward + backward (dX, dW, dBias)",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": None,
-                     "kernel": "gemm_tile_kernel (forward, bf16 " + res["path"] + ")",
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": measured_traffic(),
+                     "kernel": "gemm_pipe_kernel (forward, bf16 " + res["path"] + ")",
                      "flop_per_launch": flop},
         "extra": extra,
     }
