@@ -17,8 +17,19 @@
 
 namespace gev2 {
 
+// The direct-to-LDS kernel (gemm_dl_impl.hpp) takes 16-bit, prologue-free
+// launches with vector loads and stores on the three large tiles; GEV2_DL=0
+// selects the register-staged kernel instead (comparison runs).
+bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a) {
+  if (dtype == GEV2_F32 || !vec || pro != 0 || !a.store_vec || cfg == kCfg64x64) return false;
+  const char* v = std::getenv("GEV2_DL");
+  return !(v && v[0] == '0');
+}
+
 hipError_t launch_tile(int dtype, int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
                        int batch, hipStream_t s) {
+  if (dl_selected(dtype, cfg, pro, vec, a))
+    return dtype == GEV2_BF16 ? launch_dl_bf16(cfg, ta, tb, a, batch, s) : launch_dl_f16(cfg, ta, tb, a, batch, s);
   switch (dtype) {
     case GEV2_F32: return launch_tile_f32(cfg, ta, tb, pro, vec, a, batch, s);
     case GEV2_BF16: return launch_tile_bf16(cfg, ta, tb, pro, vec, a, batch, s);
@@ -112,8 +123,16 @@ int pick_cfg(int dtype, int64_t M, int64_t N, int64_t batch, bool fused = false)
   return best;
 }
 
-const char* cfg_name(int cfg, bool vec) {
+const char* cfg_name(int cfg, bool vec, bool dl = false) {
   if (!vec) return "tile:64x64:scalar";
+  if (dl) {
+    switch (cfg) {
+      case gev2::kCfg256x256: return "dl:256x256";
+      case gev2::kCfg128x128: return "dl:128x128";
+      case gev2::kCfg128x256: return "dl:128x256";
+      default: return "dl:?";
+    }
+  }
   switch (cfg) {
     case gev2::kCfg256x256: return "tile:256x256";
     case gev2::kCfg128x128: return "tile:128x128";
@@ -251,7 +270,7 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
     return fail(GEV2_INVALID, "grid too large");
   hipError_t e = gev2::launch_tile(d->dtype, cfg, ta, tb, 0, vec, a, batch, s);
   if (e != hipSuccess) return hip_fail(e, "tile launch");
-  t_last_path = cfg_name(cfg, vec);
+  t_last_path = cfg_name(cfg, vec, gev2::dl_selected(d->dtype, cfg, 0, vec, a));
   return GEV2_OK;
 }
 

@@ -1,0 +1,9 @@
+// Instantiations of the direct-to-LDS MFMA tile GEMM for one element type
+// (_Float16); split per type so the two compile in parallel.
+#include "gemm_dl_impl.hpp"
+
+namespace gev2 {
+hipError_t launch_dl_f16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
+  return launch_dl_cfg<_Float16>(cfg, ta, tb, a, batch, s);
+}
+}  // namespace gev2

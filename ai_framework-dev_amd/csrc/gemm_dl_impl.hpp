@@ -1,0 +1,302 @@
+// MFMA GEMM for 16-bit data with direct-to-LDS operand loads (gfx950).
+//
+// Same contract as gemm_pipe_kernel (TileArgs, tile order, vector epilogue)
+// for the prologue-free layouts, but neither operand passes through registers
+// on its way to LDS:
+//   - every operand chunk is fetched with `buffer_load_dwordx4 ... lds`, which
+//     writes a wave's 64 x 16 bytes to 1 KB of consecutive LDS at M0; the LDS
+//     layout is chosen by which global chunk each lane fetches;
+//   - an operand contiguous along K ("K rows") is stored as rows of 128 bytes
+//     of K with the 16-byte chunk index XOR-swizzled by the row, and its MFMA
+//     fragments are read with one ds_read_b128 each;
+//   - an operand contiguous along M/N ("MN rows") is stored as it lies in
+//     memory, one row per k, with the 32-byte block index XOR-swizzled by
+//     (k & 3), and its fragments are read with two ds_read_b64_tr_b16, which
+//     transpose 4x16 blocks of 16-bit elements across each 16-lane group:
+//     lane 16g+i receives element e of the 8-byte chunk addressed by lane
+//     16g+4e+i/4, at position i%4.
+// No VALU transpose, no ds_write and no staging registers remain in the loop.
+//
+// The loads are issued from inline assembly so that the compiler does not
+// treat them as pending writes to every LDS read that follows (it would wait
+// for all outstanding loads before each transpose read).  Completion is
+// explicit instead: each wave waits for its own loads (vmcnt) before the
+// barrier that publishes a K tile.
+#pragma once
+#include "gemm_tile_impl.hpp"
+
+namespace gev2 {
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource words matching make_rsrc (raw buffer, 2^31 - 1 bytes).
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
+  r[2] = 0x7fffffff;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from rsrc + voff + soff into LDS [lds_addr + 16 * lane].
+// M0 is reserved to the compiler, which warns about the clobber; nothing else
+// in these kernels uses M0 (LDS instructions on gfx9+ do not read it), which
+// the generated code shows, so the value set here is only read by this load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const i32x4_t& rsrc, int voff, int soff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// One operand tile of ROWS (M or N extent) x BK (= 64) 16-bit elements.
+template <int ROWS, bool MNC, int NT>
+struct DlStage {
+  static constexpr int BK = 64;
+  static constexpr int BYTES = ROWS * BK * 2;
+  static constexpr int LOADS = BYTES / 1024;                  // wave instructions per tile
+  static constexpr int LPW = LOADS / (NT / 64);               // per wave
+  static constexpr int RB = MNC ? ROWS * 2 : 128;             // LDS row bytes
+  static_assert(LOADS % (NT / 64) == 0, "tile loads must divide among the waves");
+  static_assert(!MNC || RB >= 128, "MN rows need at least 4 32-byte blocks");
+
+  int voff[LPW];    // per-lane byte offset of each load at k0 = 0 (kOobOffset if outside)
+  int kpos[LPW];    // k of the lane's chunk within the tile
+
+  // mn0: tile origin along M/N; MNlim: extent; ld: leading dimension (elements)
+  __device__ __forceinline__ void init(int64_t ld, int mn0, int MNlim, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int byte = (wave * LPW + i) * 1024 + lane * 16;   // LDS byte this lane fills
+      const int row = byte / RB, off = byte % RB;
+      if constexpr (!MNC) {
+        // row = M/N index within the tile; logical chunk = physical ^ swizzle
+        const int c = (off / 16) ^ swz(row);
+        const int mn = mn0 + row;
+        kpos[i] = c * 8;
+        voff[i] = mn < MNlim ? static_cast<int>(((int64_t)mn * ld + c * 8) * 2) : kOobOffset;
+      } else {
+        // row = k within the tile; logical 32-byte block = physical ^ (k & 3)
+        const int lb = (off / 32) ^ (row & 3);
+        const int n = lb * 16 + ((off / 16) & 1) * 8;
+        const int mn = mn0 + n;
+        kpos[i] = row;
+        voff[i] = mn < MNlim ? static_cast<int>(((int64_t)row * ld + mn) * 2) : kOobOffset;
+      }
+    }
+  }
+
+  // Byte offset of K tile k0 from the tile's k = 0 (uniform).
+  __device__ __forceinline__ static int kbytes(int k0, int64_t ld) {
+    return MNC ? static_cast<int>(k0 * ld * 2) : k0 * 2;
+  }
+
+  // Issue load I of the K tile at k0 into the LDS buffer at `buf` (uniform).
+  template <int I>
+  __device__ __forceinline__ void load(const i32x4_t& rsrc, uint32_t buf, int wave, int k0, int Klim,
+                                       int kb) const {
+    const int off = (k0 + kpos[I] < Klim) ? voff[I] : kOobOffset;
+    dma16(rsrc, off, kb, buf + (wave * LPW + I) * 1024);
+  }
+
+  // MFMA fragment (8 elements of k16 step q) for rows/cols [r0, r0 + 32).
+  __device__ __forceinline__ u32x4 frag(const char* buf, int r0, int q, int lane) const {
+    if constexpr (!MNC) {
+      const int row = r0 + (lane & 31);
+      const int ch = 2 * q + (lane >> 5);
+      return *reinterpret_cast<const u32x4*>(buf + row * 128 + ((ch ^ swz(row)) * 16));
+    } else {
+      const int g = lane >> 4, e = (lane >> 2) & 3, qq = lane & 3;
+      const int n = r0 + 16 * (g & 1) + 4 * qq;
+      u32x4 out;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 16 * q + 8 * (g >> 1) + 4 * h + e;
+        const char* p = buf + k * RB + (((n >> 4) ^ (k & 3)) << 5) + (n & 15) * 2;
+        const s16x4_t v =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p));
+        const u32x2 w = __builtin_bit_cast(u32x2, v);
+        out[2 * h] = w[0];
+        out[2 * h + 1] = w[1];
+      }
+      return out;
+    }
+  }
+};
+
+template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_dl_kernel(TileArgs p) {
+  static_assert(sizeof(T) == 2, "16-bit element types only");
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int NMF = FM * FN, NFR = FM + FN;
+  constexpr int H = (NMF + 1) / 2;
+  using SA = DlStage<BM, TA, NT>;
+  using SB = DlStage<BN, !TB, NT>;
+  constexpr int ABYTES = SA::BYTES, BBYTES = SB::BYTES;
+
+  __shared__ __attribute__((aligned(1024))) char lds[2 * (ABYTES + BBYTES)];
+  char* As = lds;
+  char* Bs = lds + 2 * ABYTES;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM, wn = wave / WM;
+  int tm, tn;
+  map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int bz = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const i32x4_t rA = rsrc_words(reinterpret_cast<const T*>(p.A) + (int64_t)bz * p.sA);
+  const i32x4_t rB = rsrc_words(reinterpret_cast<const T*>(p.B) + (int64_t)bz * p.sB);
+  SA sa;
+  SB sb;
+  sa.init(p.lda, m0, p.M, wave, lane);
+  sb.init(p.ldb, n0, p.N, wave, lane);
+  const uint32_t a_lds = lds_addr(As), b_lds = lds_addr(Bs);
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int KT = (p.K + BK - 1) / BK;
+  constexpr int NL = SA::LPW + SB::LPW;   // load instructions per wave per tile
+  static_assert(NL <= 63, "vmcnt range");
+  auto load_one = [&]<int L>(int buf, int k0, int kba, int kbb) __attribute__((always_inline)) {
+    if constexpr (L < SA::LPW) sa.template load<L>(rA, a_lds + buf * ABYTES, wave, k0, p.K, kba);
+    else sb.template load<L - SA::LPW>(rB, b_lds + buf * BBYTES, wave, k0, p.K, kbb);
+  };
+  auto read_one = [&]<int F>(int buf, int q, u32x4 (&af)[FM], u32x4 (&bfr)[FN]) __attribute__((always_inline)) {
+    if constexpr (F < FM) af[F] = sa.frag(As + buf * ABYTES, wm * WTM + F * 32, q, lane);
+    else bfr[F - FM] = sb.frag(Bs + buf * BBYTES, wn * WTN + (F - FM) * 32, q, lane);
+  };
+  auto mfma_one = [&]<int X>(const u32x4 (&af)[FM], const u32x4 (&bfr)[FN]) __attribute__((always_inline)) {
+    constexpr int I = X / FN, J = X % FN;
+    mfma_step<T>(acc[I][J], af[I], bfr[J]);
+  };
+
+  // Two LDS buffers: tile t in buffer t % 2.
+  //   q0..q2: MFMAs of steps 0..2 | fragment reads of steps 1..3
+  //   wait for this wave's loads of tile t+1, barrier (tile t+1 complete in
+  //   LDS; every wave done with buffer t % 2)
+  //   q3: MFMAs of step 3 | step-0 reads of tile t+1 | loads of tile t+2
+  //   into buffer t % 2
+  static_for<0, NL>([&]<int L>() __attribute__((always_inline)) {
+    load_one.template operator()<L>(0, 0, 0, 0);
+  });
+  static_for<0, NL>([&]<int L>() __attribute__((always_inline)) {
+    load_one.template operator()<L>(1, BK, SA::kbytes(BK, p.lda), SB::kbytes(BK, p.ldb));
+  });
+  // vmcnt(NL): this wave's loads of tile 0 have landed
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+  __syncthreads();
+  u32x4 af[2][FM], bfr[2][FN];
+  static_for<0, NFR>([&]<int F>() __attribute__((always_inline)) {
+    read_one.template operator()<F>(0, 0, af[0], bfr[0]);
+  });
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
+      mfma_one.template operator()<X>(af[0], bfr[0]);
+      if constexpr (X < H)
+        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
+          read_one.template operator()<F>(cur, 1, af[1], bfr[1]);
+        });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
+      mfma_one.template operator()<X>(af[1], bfr[1]);
+      if constexpr (X < H)
+        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
+          read_one.template operator()<F>(cur, 2, af[0], bfr[0]);
+        });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
+      mfma_one.template operator()<X>(af[0], bfr[0]);
+      if constexpr (X < H)
+        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
+          read_one.template operator()<F>(cur, 3, af[1], bfr[1]);
+        });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    __builtin_amdgcn_s_waitcnt(0x3f70);   // vmcnt(0): this wave's loads of tile t+1 are in LDS
+    __syncthreads();
+    const int kload = (kt + 2) * BK;
+    const int kba = SA::kbytes(kload, p.lda), kbb = SB::kbytes(kload, p.ldb);
+    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
+      mfma_one.template operator()<X>(af[1], bfr[1]);
+      if constexpr (X < H)
+        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
+          read_one.template operator()<F>(cur ^ 1, 0, af[0], bfr[0]);
+        });
+      static_for<X * NL / NMF, (X + 1) * NL / NMF>([&]<int L>() __attribute__((always_inline)) {
+        load_one.template operator()<L>(cur, kload, kba, kbb);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70);   // the loads of the last two iterations (all out of range)
+
+  // epilogue (vector stores: the host selects this kernel only with store_vec)
+  float* bias_lds = reinterpret_cast<float*>(lds);
+  __syncthreads();
+  if (p.bias && p.bias_kind == kBiasPerN) {
+    const float* biasb = p.bias + (int64_t)bz * p.sBias;
+    for (int c = tid; c < BN; c += NT) bias_lds[c] = n0 + c < p.N ? biasb[n0 + c] : 0.f;
+  }
+  __syncthreads();
+  dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+    store_tile_vec<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds);
+  });
+}
+
+template <typename T, int CFG, bool TA, bool TB>
+static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
+  using C = CfgShape<CFG>;
+  dim3 grid(a.tiles_m * a.tiles_n, batch);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, C::WM, C::WN, TA, TB>), grid, dim3(C::WM * C::WN * 64), 0,
+                     s, a);
+  return hipGetLastError();
+}
+
+template <typename T, int CFG>
+static hipError_t launch_dl_layout(bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
+  if (!ta && !tb) return launch_dl_one<T, CFG, false, false>(a, batch, s);
+  if (!ta && tb) return launch_dl_one<T, CFG, false, true>(a, batch, s);
+  if (ta && !tb) return launch_dl_one<T, CFG, true, false>(a, batch, s);
+  return hipErrorInvalidValue;
+}
+
+// Used for 16-bit data, prologue-free layouts, 16-byte-aligned operands and
+// vector stores, on the 256x256 / 128x256 / 128x128 tiles.
+template <typename T>
+static hipError_t launch_dl_cfg(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
+  switch (cfg) {
+    case kCfg256x256: return launch_dl_layout<T, kCfg256x256>(ta, tb, a, batch, s);
+    case kCfg128x256: return launch_dl_layout<T, kCfg128x256>(ta, tb, a, batch, s);
+    case kCfg128x128: return launch_dl_layout<T, kCfg128x128>(ta, tb, a, batch, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace gev2

@@ -88,6 +88,9 @@ hipError_t launch_tile_bf16(int cfg, bool ta, bool tb, int pro, bool vec, const 
                             int batch, hipStream_t s);
 hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
                            int batch, hipStream_t s);
+hipError_t launch_dl_bf16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
+hipError_t launch_dl_f16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
+bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a);
 hipError_t launch_skinny(int dtype, const SkinnyArgs& a, hipStream_t s);
 hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const GradArgs& a, int batch, hipStream_t s);
