@@ -86,6 +86,17 @@ bool out_vec_ok(const void* p, int64_t ld, int64_t stride, int64_t rows, int64_t
   return span * static_cast<int64_t>(elem_size(dtype)) <= 0x7fffff00LL;
 }
 
+// Epilogue level of an output: 0 = scalar stores, 1 = 4-column vector
+// stores, 2 = 16-byte row segments (16-bit data with 8-column groups whose
+// starts are 16-byte aligned), which the direct-to-LDS kernel stages
+// through LDS.
+int out_level(const void* p, int64_t ld, int64_t stride, int64_t rows, int64_t cols, int batch, int dtype) {
+  if (!out_vec_ok(p, ld, stride, rows, cols, batch, dtype)) return 0;
+  if (!p) return 2;
+  if (dtype == GEV2_F32 || ld % 8 != 0 || cols % 8 != 0 || (batch > 1 && stride % 8 != 0)) return 1;
+  return 2;
+}
+
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   if (!v || !*v) return dflt;
@@ -264,8 +275,8 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
   a.tiles_m = static_cast<int>((M + bm - 1) / bm);
   a.tiles_n = static_cast<int>((N + bn - 1) / bn);
-  a.store_vec = (out_vec_ok(d->Y, ldy, d->stride_y, M, N, batch, d->dtype) &&
-                 out_vec_ok(d->Z, ldz, d->stride_z, M, N, batch, d->dtype)) ? 1 : 0;
+  a.store_vec = std::min(out_level(d->Y, ldy, d->stride_y, M, N, batch, d->dtype),
+                         out_level(d->Z, ldz, d->stride_z, M, N, batch, d->dtype));
   if (static_cast<int64_t>(a.tiles_m) * a.tiles_n > 0x7fffffffLL || batch > 65535)
     return fail(GEV2_INVALID, "grid too large");
   hipError_t e = gev2::launch_tile(d->dtype, cfg, ta, tb, 0, vec, a, batch, s);
@@ -377,7 +388,7 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
     a.tiles_m = static_cast<int>((M + bm - 1) / bm);
     a.tiles_n = static_cast<int>((K + bn - 1) / bn);
-    a.store_vec = out_vec_ok(d->gA, ldga, d->stride_ga, M, K, batch, dt) ? 1 : 0;
+    a.store_vec = out_level(d->gA, ldga, d->stride_ga, M, K, batch, dt);
     hipError_t e = gev2::launch_tile(dt, cfg, false, true, fused ? 1 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dX launch");
   }
@@ -397,7 +408,7 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
     a.tiles_m = static_cast<int>((K + bm - 1) / bm);
     a.tiles_n = static_cast<int>((N + bn - 1) / bn);
-    a.store_vec = out_vec_ok(d->gB, ldgb, d->stride_gb, K, N, batch, dt) ? 1 : 0;
+    a.store_vec = out_level(d->gB, ldgb, d->stride_gb, K, N, batch, dt);
     hipError_t e = gev2::launch_tile(dt, cfg, true, false, fused ? 2 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dW launch");
   }

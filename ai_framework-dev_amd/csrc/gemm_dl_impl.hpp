@@ -6,8 +6,8 @@
 //   - every operand chunk is fetched with `buffer_load_dwordx4 ... lds`, which
 //     writes a wave's 64 x 16 bytes to 1 KB of consecutive LDS at M0; the LDS
 //     layout is chosen by which global chunk each lane fetches;
-//   - an operand contiguous along K ("K rows") is stored as rows of 128 bytes
-//     of K with the 16-byte chunk index XOR-swizzled by the row, and its MFMA
+//   - an operand contiguous along K ("K rows") is stored as rows of BK
+//     elements with the 16-byte chunk index XOR-swizzled by the row, and its MFMA
 //     fragments are read with one ds_read_b128 each;
 //   - an operand contiguous along M/N ("MN rows") is stored as it lies in
 //     memory, one row per k, with the 32-byte block index XOR-swizzled by
@@ -16,6 +16,7 @@
 //     lane 16g+i receives element e of the 8-byte chunk addressed by lane
 //     16g+4e+i/4, at position i%4.
 // No VALU transpose, no ds_write and no staging registers remain in the loop.
+// The LDS holds S stages of BK k each, so loads run S-1 tiles ahead.
 //
 // The loads are issued from inline assembly so that the compiler does not
 // treat them as pending writes to every LDS read that follows (it would wait
@@ -59,14 +60,25 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
-// One operand tile of ROWS (M or N extent) x BK (= 64) 16-bit elements.
-template <int ROWS, bool MNC, int NT>
+// Chunk swizzle of K rows.  BK = 64: 8 chunks per 128-byte row, the tile
+// kernel's swz().  BK = 32: 4 chunks per 64-byte row; ((row >> 1) ^ (row >> 3))
+// & 3 gives the rows of equal parity in any aligned 8 (and the rows of equal
+// row & 3 in any aligned 16) distinct chunk positions, so fragment reads are
+// conflict free whether a bank cycle serves 128 or 256 bytes.
+template <int BK>
+__device__ __forceinline__ int swz_k(int row) {
+  if constexpr (BK == 64) return swz(row);
+  else return ((row >> 1) ^ (row >> 3)) & 3;
+}
+
+// One operand tile of ROWS (M or N extent) x BK (32 or 64) 16-bit elements.
+template <int ROWS, bool MNC, int NT, int BK>
 struct DlStage {
-  static constexpr int BK = 64;
+  static_assert(BK == 32 || BK == 64, "BK");
   static constexpr int BYTES = ROWS * BK * 2;
   static constexpr int LOADS = BYTES / 1024;                  // wave instructions per tile
   static constexpr int LPW = LOADS / (NT / 64);               // per wave
-  static constexpr int RB = MNC ? ROWS * 2 : 128;             // LDS row bytes
+  static constexpr int RB = MNC ? ROWS * 2 : BK * 2;          // LDS row bytes
   static_assert(LOADS % (NT / 64) == 0, "tile loads must divide among the waves");
   static_assert(!MNC || RB >= 128, "MN rows need at least 4 32-byte blocks");
 
@@ -81,7 +93,7 @@ struct DlStage {
       const int row = byte / RB, off = byte % RB;
       if constexpr (!MNC) {
         // row = M/N index within the tile; logical chunk = physical ^ swizzle
-        const int c = (off / 16) ^ swz(row);
+        const int c = (off / 16) ^ swz_k<BK>(row);
         const int mn = mn0 + row;
         kpos[i] = c * 8;
         voff[i] = mn < MNlim ? static_cast<int>(((int64_t)mn * ld + c * 8) * 2) : kOobOffset;
@@ -114,7 +126,7 @@ struct DlStage {
     if constexpr (!MNC) {
       const int row = r0 + (lane & 31);
       const int ch = 2 * q + (lane >> 5);
-      return *reinterpret_cast<const u32x4*>(buf + row * 128 + ((ch ^ swz(row)) * 16));
+      return *reinterpret_cast<const u32x4*>(buf + row * RB + ((ch ^ swz_k<BK>(row)) * 16));
     } else {
       const int g = lane >> 4, e = (lane >> 2) & 3, qq = lane & 3;
       const int n = r0 + 16 * (g & 1) + 4 * qq;
@@ -134,23 +146,102 @@ struct DlStage {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB>
+// Epilogue through LDS (16-bit outputs with 16-byte aligned rows, N % 8 == 0).
+// The MFMA result layout gives each lane 4 consecutive columns of one row, so
+// a direct store writes 8-byte pieces of 32 different rows.  Instead each wave
+// converts one 32-row slab of its results to 16-bit values in its own LDS
+// region (16-byte chunks XOR-swizzled by row), then reads it back row-major
+// and writes 16 bytes per lane with consecutive lanes on consecutive bytes of
+// a row.  Only the wave's own region is touched, and LDS instructions of one
+// wave execute in order, so no barrier is needed between the two phases.
+template <typename T, int FM, int FN, int WTM, int WTN, int ACT>
+__device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FM][FN], const TileArgs& p, int bz, int m0,
+                                               int n0, int wm, int wn, int lane, const float* bias_lds,
+                                               char* stage) {
+  constexpr int RBY = WTN * 2;     // bytes per staged row
+  constexpr int CPR = RBY / 16;    // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;    // rows per read-back instruction
+  static_assert(64 % CPR == 0 && 32 % RPI == 0, "staged row shape");
+  char* ys = stage;
+  char* zs = stage + 32 * RBY;
+  const __amdgpu_buffer_rsrc_t rD = make_rsrc(reinterpret_cast<T*>(p.D) + (int64_t)bz * p.sD);
+  const bool hz = p.Zo != nullptr;
+  const __amdgpu_buffer_rsrc_t rZ = make_rsrc(hz ? reinterpret_cast<T*>(p.Zo) + (int64_t)bz * p.sZo
+                                                 : reinterpret_cast<T*>(p.D));
+  const float* biasb = p.bias ? p.bias + (int64_t)bz * p.sBias : nullptr;
+  const int bk = biasb ? p.bias_kind : kBiasNone;
+  const float alpha = p.alpha;
+  const float bscalar = bk == kBiasScalar ? biasb[0] : 0.f;
+  const int h = lane >> 5, rr = lane & 31;
+  static_for<0, FM>([&]<int I>() __attribute__((always_inline)) {
+    const int mw = m0 + wm * WTM + I * 32;   // first row of the slab
+    const float brow = bk == kBiasPerM ? (mw + rr < p.M ? biasb[mw + rr] : 0.f) : bscalar;
+    static_for<0, FN * 4>([&]<int JQ>() __attribute__((always_inline)) {
+      constexpr int J = JQ / 4, Q = JQ % 4;
+      const int nl = wn * WTN + J * 32 + Q * 8 + h * 4;   // column within the tile
+      f32x4_t bv = {brow, brow, brow, brow};
+      if (bk == kBiasPerN) bv = *reinterpret_cast<const f32x4_t*>(bias_lds + nl);
+      float pre[4], y[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        pre[t] = fmaf(alpha, acc[I][J][Q * 4 + t], bv[t]);
+        y[t] = act_fwd_t<ACT>(pre[t], p.slope);
+      }
+      const int off = rr * RBY + (((J * 4 + Q) ^ (rr & (CPR - 1))) * 16) + h * 8;
+      *reinterpret_cast<u32x2*>(ys + off) = u32x2{Elem<T>::bits(y[0]) | (Elem<T>::bits(y[1]) << 16),
+                                                  Elem<T>::bits(y[2]) | (Elem<T>::bits(y[3]) << 16)};
+      if (hz)
+        *reinterpret_cast<u32x2*>(zs + off) = u32x2{Elem<T>::bits(pre[0]) | (Elem<T>::bits(pre[1]) << 16),
+                                                    Elem<T>::bits(pre[2]) | (Elem<T>::bits(pre[3]) << 16)};
+    });
+    asm volatile("" ::: "memory");
+    static_for<0, 32 / RPI>([&]<int R>() __attribute__((always_inline)) {
+      const int row = R * RPI + lane / CPR, ch = lane % CPR;
+      const int off = row * RBY + ((ch ^ (row & (CPR - 1))) * 16);
+      const int m = mw + row;
+      const int n = n0 + wn * WTN + ch * 8;
+      const bool ok = m < p.M && n < p.N;
+      const u32x4 yv = *reinterpret_cast<const u32x4*>(ys + off);
+      __builtin_amdgcn_raw_buffer_store_b128(yv, rD, ok ? static_cast<int>(((int64_t)m * p.ldd + n) * 2) : kOobOffset,
+                                             0, 0);
+      if (hz) {
+        const u32x4 zv = *reinterpret_cast<const u32x4*>(zs + off);
+        __builtin_amdgcn_raw_buffer_store_b128(zv, rZ, ok ? static_cast<int>(((int64_t)m * p.ldzo + n) * 2) : kOobOffset,
+                                               0, 0);
+      }
+    });
+    asm volatile("" ::: "memory");
+  });
+}
+
+// S LDS stages of BK k each; tile t lives in stage t % S.  Per tile:
+//   q = 0 .. NQ-2: MFMAs of step q | fragment reads of step q+1
+//   wait for this wave's loads of tile t+1 (the S-2 younger tiles stay in
+//   flight), barrier: tile t+1 is complete in LDS and every wave is done
+//   reading stage t % S
+//   q = NQ-1: MFMAs of the last step | step-0 reads of tile t+1 | loads of
+//   tile t+S into stage t % S
+// so a tile's loads are issued S-1 tiles before it is read.
+template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_dl_kernel(TileArgs p) {
   static_assert(sizeof(T) == 2, "16-bit element types only");
   constexpr int NT = WM * WN * 64;
-  constexpr int BK = 64;
+  constexpr int NQ = BK / 16;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
   constexpr int NMF = FM * FN, NFR = FM + FN;
   constexpr int H = (NMF + 1) / 2;
-  using SA = DlStage<BM, TA, NT>;
-  using SB = DlStage<BN, !TB, NT>;
+  using SA = DlStage<BM, TA, NT, BK>;
+  using SB = DlStage<BN, !TB, NT, BK>;
   constexpr int ABYTES = SA::BYTES, BBYTES = SB::BYTES;
+  constexpr int NL = SA::LPW + SB::LPW;   // load instructions per wave per tile
+  static_assert(S >= 2 && (S - 1) * NL <= 63, "vmcnt range");
+  static_assert(S * (ABYTES + BBYTES) <= 160 * 1024, "LDS");
 
-  __shared__ __attribute__((aligned(1024))) char lds[2 * (ABYTES + BBYTES)];
+  __shared__ __attribute__((aligned(1024))) char lds[S * (ABYTES + BBYTES)];
   char* As = lds;
-  char* Bs = lds + 2 * ABYTES;
+  char* Bs = lds + S * ABYTES;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -178,86 +269,68 @@ gemm_dl_kernel(TileArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int KT = (p.K + BK - 1) / BK;
-  constexpr int NL = SA::LPW + SB::LPW;   // load instructions per wave per tile
-  static_assert(NL <= 63, "vmcnt range");
-  auto load_one = [&]<int L>(int buf, int k0, int kba, int kbb) __attribute__((always_inline)) {
-    if constexpr (L < SA::LPW) sa.template load<L>(rA, a_lds + buf * ABYTES, wave, k0, p.K, kba);
-    else sb.template load<L - SA::LPW>(rB, b_lds + buf * BBYTES, wave, k0, p.K, kbb);
+  auto load_one = [&]<int L>(int st, int k0, int kba, int kbb) __attribute__((always_inline)) {
+    if constexpr (L < SA::LPW) sa.template load<L>(rA, a_lds + st * ABYTES, wave, k0, p.K, kba);
+    else sb.template load<L - SA::LPW>(rB, b_lds + st * BBYTES, wave, k0, p.K, kbb);
   };
-  auto read_one = [&]<int F>(int buf, int q, u32x4 (&af)[FM], u32x4 (&bfr)[FN]) __attribute__((always_inline)) {
-    if constexpr (F < FM) af[F] = sa.frag(As + buf * ABYTES, wm * WTM + F * 32, q, lane);
-    else bfr[F - FM] = sb.frag(Bs + buf * BBYTES, wn * WTN + (F - FM) * 32, q, lane);
+  auto load_tile = [&](int st, int k0) __attribute__((always_inline)) {
+    const int kba = SA::kbytes(k0, p.lda), kbb = SB::kbytes(k0, p.ldb);
+    static_for<0, NL>([&]<int L>() __attribute__((always_inline)) { load_one.template operator()<L>(st, k0, kba, kbb); });
+  };
+  auto read_one = [&]<int F>(int st, int q, u32x4 (&af)[FM], u32x4 (&bfr)[FN]) __attribute__((always_inline)) {
+    if constexpr (F < FM) af[F] = sa.frag(As + st * ABYTES, wm * WTM + F * 32, q, lane);
+    else bfr[F - FM] = sb.frag(Bs + st * BBYTES, wn * WTN + (F - FM) * 32, q, lane);
   };
   auto mfma_one = [&]<int X>(const u32x4 (&af)[FM], const u32x4 (&bfr)[FN]) __attribute__((always_inline)) {
     constexpr int I = X / FN, J = X % FN;
     mfma_step<T>(acc[I][J], af[I], bfr[J]);
   };
 
-  // Two LDS buffers: tile t in buffer t % 2.
-  //   q0..q2: MFMAs of steps 0..2 | fragment reads of steps 1..3
-  //   wait for this wave's loads of tile t+1, barrier (tile t+1 complete in
-  //   LDS; every wave done with buffer t % 2)
-  //   q3: MFMAs of step 3 | step-0 reads of tile t+1 | loads of tile t+2
-  //   into buffer t % 2
-  static_for<0, NL>([&]<int L>() __attribute__((always_inline)) {
-    load_one.template operator()<L>(0, 0, 0, 0);
-  });
-  static_for<0, NL>([&]<int L>() __attribute__((always_inline)) {
-    load_one.template operator()<L>(1, BK, SA::kbytes(BK, p.lda), SB::kbytes(BK, p.ldb));
-  });
-  // vmcnt(NL): this wave's loads of tile 0 have landed
-  __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+  static_for<0, S>([&]<int P>() __attribute__((always_inline)) { load_tile(P, P * BK); });
+  // vmcnt((S-1) * NL): this wave's loads of tile 0 have landed
+  constexpr int kWaitFirst = (S - 1) * NL, kWaitLoop = (S - 2) * NL;
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (kWaitFirst & 0xf) | ((kWaitFirst >> 4) << 14));
   __syncthreads();
   u32x4 af[2][FM], bfr[2][FN];
   static_for<0, NFR>([&]<int F>() __attribute__((always_inline)) {
     read_one.template operator()<F>(0, 0, af[0], bfr[0]);
   });
 
+  int cur = 0;   // stage of tile kt
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
-      mfma_one.template operator()<X>(af[0], bfr[0]);
-      if constexpr (X < H)
-        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
-          read_one.template operator()<F>(cur, 1, af[1], bfr[1]);
-        });
-      __builtin_amdgcn_sched_barrier(0);
+    const int nxt = cur + 1 == S ? 0 : cur + 1;
+    static_for<0, NQ - 1>([&]<int Q>() __attribute__((always_inline)) {
+      static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
+        mfma_one.template operator()<X>(af[Q & 1], bfr[Q & 1]);
+        if constexpr (X < H)
+          static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
+            read_one.template operator()<F>(cur, Q + 1, af[(Q + 1) & 1], bfr[(Q + 1) & 1]);
+          });
+        __builtin_amdgcn_sched_barrier(0);
+      });
     });
-    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
-      mfma_one.template operator()<X>(af[1], bfr[1]);
-      if constexpr (X < H)
-        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
-          read_one.template operator()<F>(cur, 2, af[0], bfr[0]);
-        });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
-      mfma_one.template operator()<X>(af[0], bfr[0]);
-      if constexpr (X < H)
-        static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
-          read_one.template operator()<F>(cur, 3, af[1], bfr[1]);
-        });
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    __builtin_amdgcn_s_waitcnt(0x3f70);   // vmcnt(0): this wave's loads of tile t+1 are in LDS
+    __builtin_amdgcn_s_waitcnt(0x3f70 | (kWaitLoop & 0xf) | ((kWaitLoop >> 4) << 14));
     __syncthreads();
-    const int kload = (kt + 2) * BK;
+    const int kload = (kt + S) * BK;
     const int kba = SA::kbytes(kload, p.lda), kbb = SB::kbytes(kload, p.ldb);
+    constexpr int QL = (NQ - 1) & 1;
     static_for<0, NMF>([&]<int X>() __attribute__((always_inline)) {
-      mfma_one.template operator()<X>(af[1], bfr[1]);
+      mfma_one.template operator()<X>(af[QL], bfr[QL]);
       if constexpr (X < H)
         static_for<X * NFR / H, (X + 1) * NFR / H>([&]<int F>() __attribute__((always_inline)) {
-          read_one.template operator()<F>(cur ^ 1, 0, af[0], bfr[0]);
+          read_one.template operator()<F>(nxt, 0, af[0], bfr[0]);
         });
       static_for<X * NL / NMF, (X + 1) * NL / NMF>([&]<int L>() __attribute__((always_inline)) {
         load_one.template operator()<L>(cur, kload, kba, kbb);
       });
       __builtin_amdgcn_sched_barrier(0);
     });
+    cur = nxt;
   }
-  __builtin_amdgcn_s_waitcnt(0x3f70);   // the loads of the last two iterations (all out of range)
+  __builtin_amdgcn_s_waitcnt(0x3f70);   // the loads past the last tile (all out of range)
 
-  // epilogue (vector stores: the host selects this kernel only with store_vec)
+  // epilogue (the host selects this kernel only with store_vec: 2 = 16-bit
+  // rows with 16-byte aligned starts and N % 8 == 0, staged through LDS)
   float* bias_lds = reinterpret_cast<float*>(lds);
   __syncthreads();
   if (p.bias && p.bias_kind == kBiasPerN) {
@@ -265,17 +338,39 @@ gemm_dl_kernel(TileArgs p) {
     for (int c = tid; c < BN; c += NT) bias_lds[c] = n0 + c < p.N ? biasb[n0 + c] : 0.f;
   }
   __syncthreads();
-  dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
-    store_tile_vec<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds);
-  });
+  if (p.store_vec == 2) {
+    static_assert(1024 + NT / 64 * 64 * WTN * 2 <= S * (ABYTES + BBYTES), "epilogue staging");
+    char* stage = lds + 1024 + wave * (64 * WTN * 2);
+    dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+      store_tile_lds<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds, stage);
+    });
+  } else {
+    dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+      store_tile_vec<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds);
+    });
+  }
 }
+
+// K depth and stage count per tile shape: the most stages of BK = 32 that fit
+// in LDS (two 128x128 workgroups share a CU).
+// GEV2_DL256_BK / GEV2_DL256_S override the 256x256 choice at build time
+// (tuning builds).
+#ifndef GEV2_DL256_BK
+#define GEV2_DL256_BK 64
+#define GEV2_DL256_S 2
+#endif
+template <int CFG> struct DlPipe;
+template <> struct DlPipe<kCfg256x256> { static constexpr int BK = GEV2_DL256_BK, S = GEV2_DL256_S; };
+template <> struct DlPipe<kCfg128x256> { static constexpr int BK = 32, S = 6; };
+template <> struct DlPipe<kCfg128x128> { static constexpr int BK = 32, S = 4; };
 
 template <typename T, int CFG, bool TA, bool TB>
 static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
   using C = CfgShape<CFG>;
+  using P = DlPipe<CFG>;
   dim3 grid(a.tiles_m * a.tiles_n, batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, C::WM, C::WN, TA, TB>), grid, dim3(C::WM * C::WN * 64), 0,
-                     s, a);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, C::WM, C::WN, TA, TB, P::BK, P::S>), grid,
+                     dim3(C::WM * C::WN * 64), 0, s, a);
   return hipGetLastError();
 }
 

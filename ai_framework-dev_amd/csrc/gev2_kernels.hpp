@@ -27,7 +27,7 @@ struct TileArgs {
   float slope, alpha;
   int pro_act;           // prologue activation kind (derivative applied)
   int tiles_m, tiles_n;
-  int store_vec;         // D/Zo rows allow 4-wide vector stores
+  int store_vec;         // D/Zo rows: 0 scalar, 1 4-wide vector stores, 2 16-byte row segments (16-bit)
 };
 
 // Skinny forward (M <= kSkinnyMaxM): one workgroup per 32-byte column slab of

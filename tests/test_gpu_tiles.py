@@ -1,0 +1,92 @@
+"""GPU parity of every large-tile kernel variant, forced one at a time.
+
+The tile dispatcher picks the kernel by cost; here GEV2_TILE_CFG pins the tile
+(256x256, 128x256, 128x128) so that each shape runs through each variant:
+the direct-to-LDS kernel for 16-bit data (both epilogue forms: LDS-staged
+16-byte rows when N % 8 == 0, 4-column stores when only N % 4 == 0), and
+with GEV2_DL=0 the register-staged kernel it replaces.
+
+Inputs are small integers, so every dot product is exact in fp32 and the
+device result must equal the oracle's after one rounding to the storage type,
+bit for bit (reference semantics: launcher.cu:147-274, epilogue traits.hpp:43-71).
+Shapes are ragged against every tile (M, N) and against BK = 32 and 64 (K).
+"""
+import numpy as np
+import pytest
+
+from oracle import gemm_oracle as O
+from gemm_helpers import BF16, F16, DT_NAMES, Dev, rounded
+
+pytestmark = pytest.mark.gpu
+
+CFGS = {0: "256x256", 3: "128x256", 1: "128x128"}
+
+# (layout, M, N, K, ldy_pad): NT keeps K contiguous on both operands, so N may
+# be 4 mod 8 there (the 4-column epilogue); NN / TN need N (and TN M) % 8 == 0
+# for vector loads.  ldy_pad = 4 makes the output rows 8-byte aligned only.
+CASES = [
+    ("NN", 300, 264, 328, 0),
+    ("NT", 300, 264, 328, 0),
+    ("TN", 296, 264, 328, 0),
+    ("NT", 300, 268, 328, 0),
+    ("NN", 300, 264, 200, 4),
+    ("NN", 520, 1040, 96, 0),
+]
+
+
+def _ints(g, shape, lo=-2, hi=2):
+    return g.integers(lo, hi + 1, size=shape).astype(np.float32)
+
+
+def _run(capi, layout, M, N, K, ldy_pad, dtype, bias_kind, act, seed):
+    g = np.random.default_rng(seed)
+    X = _ints(g, (M, K))
+    W = _ints(g, (K, N))
+    nb = {O.BIAS_PERN: N, O.BIAS_PERM: M, O.BIAS_SCALAR: 1}[bias_kind]
+    b = _ints(g, (nb,), -3, 3)
+    ta, tb = layout[0] == "T", layout[1] == "T"
+    A = np.ascontiguousarray(X.T) if ta else X
+    B = np.ascontiguousarray(W.T) if tb else W
+    ldy = N + ldy_pad
+    es = capi.elem_bytes(dtype)
+    dev = Dev(capi)
+    try:
+        pA, pB = dev.put(capi.to_storage(A, dtype)), dev.put(capi.to_storage(B, dtype))
+        pb = dev.put(b)
+        pY = dev.empty(M * ldy * es)
+        pZ = dev.empty(M * ldy * es)
+        capi.gemm_fwd(dtype=dtype, M=M, N=N, K=K, A=pA, B=pB, Y=pY, Z=pZ, bias=pb, bias_kind=bias_kind,
+                      act=act, trans_a=ta, trans_b=tb, ldy=ldy, ldz=ldy)
+        path = capi.last_path()
+        capi.synchronize()
+        Y = dev.get(pY, (M, ldy), dtype)[:, :N]
+        Z = dev.get(pZ, (M, ldy), dtype)[:, :N]
+    finally:
+        dev.close()
+    Y64, Z64 = O.gemm_forward(X, W, b, bias_kind, act)
+    return Y, Z, rounded(Y64, dtype), rounded(Z64, dtype), path
+
+
+@pytest.mark.parametrize("cfg", list(CFGS), ids=lambda c: CFGS[c])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}-pad{c[4]}")
+@pytest.mark.parametrize("kernel", ["dl", "pipe"])
+def test_tile_variants_exact(gpu, monkeypatch, cfg, case, kernel):
+    capi = gpu
+    monkeypatch.setenv("GEV2_TILE_CFG", str(cfg))
+    monkeypatch.setenv("GEV2_DL", "1" if kernel == "dl" else "0")
+    layout, M, N, K, pad = case
+    Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, BF16, O.BIAS_PERN, "relu", seed=cfg * 7 + M)
+    assert path == f"{'dl' if kernel == 'dl' else 'tile'}:{CFGS[cfg]}", path
+    assert np.array_equal(Z, Zr), f"Z {layout} {M}x{N}x{K} {path}"
+    assert np.array_equal(Y, Yr), f"Y {layout} {M}x{N}x{K} {path}"
+
+
+@pytest.mark.parametrize("bias_kind", [O.BIAS_PERM, O.BIAS_SCALAR])
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=lambda d: DT_NAMES[d])
+def test_dl_bias_kinds_exact(gpu, monkeypatch, bias_kind, dtype):
+    capi = gpu
+    monkeypatch.setenv("GEV2_TILE_CFG", "0")
+    Y, Z, Yr, Zr, path = _run(capi, "NN", 300, 264, 328, 0, dtype, bias_kind, "relu", seed=5)
+    assert path == "dl:256x256", path
+    assert np.array_equal(Z, Zr)
+    assert np.array_equal(Y, Yr)
