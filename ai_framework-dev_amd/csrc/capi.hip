@@ -155,22 +155,23 @@ const char* cfg_name(int cfg, bool vec, bool dl = false) {
 
 std::mutex g_ws_mu;
 
-// dY' workspace of the backward for non-linear activations, one per
-// (device, stream), grown on demand.  hipFree waits for queued work that may
-// still read the old buffer.
-std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_grad_ws;
+// Scratch for the forward's split-K partial sums and the backward's dY' when
+// the caller passes no workspace: one buffer per (device, stream), grown on
+// demand (a stream runs its calls in order, so they can share it).  hipFree
+// waits for queued work that may still read the old buffer.
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_stream_ws;
 
-int get_grad_ws(hipStream_t s, size_t bytes, void** out) {
+int get_stream_ws(hipStream_t s, size_t bytes, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto& ws = g_grad_ws[{dev, s}];
+  auto& ws = g_stream_ws[{dev, s}];
   if (ws.second < bytes) {
     if (ws.first) (void)hipFree(ws.first);
     ws = {nullptr, 0};
     e = hipMalloc(&ws.first, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(dY' workspace)");
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
     ws.second = bytes;
   }
   *out = ws.first;
@@ -191,6 +192,53 @@ int check_common(int dtype, int act, int bias_kind, int64_t M, int64_t N, int64_
 
 int64_t dense_ld(int64_t ld, int64_t cols) { return ld == 0 ? cols : ld; }
 
+// Validation and path choice of a forward call, shared by gev2_gemm_fwd and
+// gev2_gemm_fwd_workspace_size so that the size query always matches the call.
+struct FwdPlan {
+  bool empty = false;     // M == 0 or N == 0: nothing to launch
+  bool skinny = false, split = false;
+  int64_t lda = 0, ldb = 0, ldy = 0, ldz = 0;
+  int64_t ws_bytes = 0;
+  gev2::SkinnyArgs sk{};
+};
+
+int plan_fwd(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
+  if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
+  int st = check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch);
+  if (st != GEV2_OK) return st;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  if (!d->Y) return fail(GEV2_MISSING_OUTPUT, "Y is null");
+  if (K > 0 && (!d->A || !d->B)) return fail(GEV2_MISSING_INPUT, "A/B is null");
+  if (M == 0 || N == 0) {
+    pl->empty = true;
+    return GEV2_OK;
+  }
+  const bool ta = d->trans_a != 0, tb = d->trans_b != 0;
+  pl->lda = dense_ld(d->lda, ta ? M : K);
+  pl->ldb = dense_ld(d->ldb, tb ? K : N);
+  pl->ldy = dense_ld(d->ldy, N);
+  pl->ldz = dense_ld(d->ldz, N);
+  if (pl->lda < (ta ? M : K) || pl->ldb < (tb ? K : N) || pl->ldy < N || (d->Z && pl->ldz < N))
+    return fail(GEV2_STRIDE_MISMATCH, "leading dimension smaller than the row length");
+  const int epc = elems_per_chunk(d->dtype);
+  pl->skinny = d->batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 && N % epc == 0 &&
+               vec_ok(d->B, pl->ldb, 0, N, K, 1, d->dtype) && env_int("GEV2_NO_SKINNY", 0) == 0;
+  if (!pl->skinny) return GEV2_OK;
+  const bool has_bias = d->bias && d->bias_kind != GEV2_BIAS_NONE;
+  gev2::SkinnyArgs& a = pl->sk;
+  a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z;
+  a.bias = has_bias ? d->bias : nullptr;
+  a.lda = pl->lda; a.ldb = pl->ldb; a.ldd = pl->ldy; a.ldzo = pl->ldz;
+  a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
+  a.act = d->act; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
+  a.slope = d->leaky_slope; a.alpha = d->alpha;
+  a.x_vec = (aligned16(d->A) && pl->lda % epc == 0 && K % epc == 0)
+                ? (vec_ok(d->A, pl->lda, 0, K, M, 1, d->dtype) ? 2 : 1) : 0;
+  pl->split = d->dtype != GEV2_F32 && gev2::skinny_split_eligible(a);
+  pl->ws_bytes = pl->split ? gev2::skinny_split_workspace_bytes(a.M, a.N, a.K) : 0;
+  return GEV2_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -198,6 +246,13 @@ extern "C" {
 int gev2_abi_version(void) { return GEV2_ABI_VERSION; }
 
 const char* gev2_last_error(void) { return t_last_error.c_str(); }
+
+int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* d) {
+  t_last_error.clear();
+  FwdPlan pl;
+  if (plan_fwd(d, &pl) != GEV2_OK) return -1;
+  return (pl.empty || !pl.skinny) ? 0 : pl.ws_bytes;
+}
 const char* gev2_last_path(void) { return t_last_path; }
 
 const char* gev2_status_string(int s) {
@@ -222,39 +277,33 @@ const char* gev2_status_string(int s) {
 
 int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   t_last_error.clear();
-  if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
-  int st = check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch);
-  if (st != GEV2_OK) return st;
+  FwdPlan pl;
+  int st = plan_fwd(d, &pl);
+  if (st != GEV2_OK || pl.empty) return st;
   const int64_t M = d->M, N = d->N, K = d->K;
   const int batch = static_cast<int>(d->batch);
-  if (!d->Y) return fail(GEV2_MISSING_OUTPUT, "Y is null");
-  if (K > 0 && (!d->A || !d->B)) return fail(GEV2_MISSING_INPUT, "A/B is null");
-  if (M == 0 || N == 0) return GEV2_OK;
   const bool ta = d->trans_a != 0, tb = d->trans_b != 0;
-  const int64_t lda = dense_ld(d->lda, ta ? M : K), ldb = dense_ld(d->ldb, tb ? K : N);
-  const int64_t ldy = dense_ld(d->ldy, N), ldz = dense_ld(d->ldz, N);
-  if (lda < (ta ? M : K) || ldb < (tb ? K : N) || ldy < N || (d->Z && ldz < N))
-    return fail(GEV2_STRIDE_MISMATCH, "leading dimension smaller than the row length");
+  const int64_t lda = pl.lda, ldb = pl.ldb, ldy = pl.ldy, ldz = pl.ldz;
   const bool has_bias = d->bias && d->bias_kind != GEV2_BIAS_NONE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   // ---- skinny path ----
-  const int epc = elems_per_chunk(d->dtype);
-  const bool skinny_ok = batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 &&
-                         N % epc == 0 && vec_ok(d->B, ldb, 0, N, K, 1, d->dtype) &&
-                         env_int("GEV2_NO_SKINNY", 0) == 0;
-  if (skinny_ok) {
-    gev2::SkinnyArgs a{};
-    a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z;
-    a.bias = has_bias ? d->bias : nullptr;
-    a.lda = lda; a.ldb = ldb; a.ldd = ldy; a.ldzo = ldz;
-    a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
-    a.act = d->act; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
-    a.slope = d->leaky_slope; a.alpha = d->alpha;
-    a.x_vec = (aligned16(d->A) && lda % epc == 0 && K % epc == 0) ? 1 : 0;
-    hipError_t e = gev2::launch_skinny(d->dtype, a, s);
+  if (pl.skinny) {
+    float* part = nullptr;
+    if (pl.ws_bytes > 0) {
+      if (d->workspace && d->workspace_bytes >= pl.ws_bytes &&
+          (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
+        part = static_cast<float*>(d->workspace);
+      } else {
+        void* w = nullptr;
+        st = get_stream_ws(s, static_cast<size_t>(pl.ws_bytes), &w);
+        if (st != GEV2_OK) return st;
+        part = static_cast<float*>(w);
+      }
+    }
+    hipError_t e = gev2::launch_skinny(d->dtype, pl.sk, part, s);
     if (e != hipSuccess) return hip_fail(e, "skinny launch");
-    t_last_path = "skinny";
+    t_last_path = pl.split ? "skinny:split" : "skinny";
     return GEV2_OK;
   }
 
@@ -335,7 +384,7 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     if (d->workspace && d->workspace_bytes >= need && (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
       ws = d->workspace;
     } else {
-      st = get_grad_ws(s, static_cast<size_t>(need), &ws);
+      st = get_stream_ws(s, static_cast<size_t>(need), &ws);
       if (st != GEV2_OK) return st;
     }
     float* partial = sums ? reinterpret_cast<float*>(static_cast<char*>(ws) + gz_bytes) : nullptr;
@@ -515,11 +564,11 @@ int gev2_stream_create(void** stream) {
 int gev2_stream_destroy(void* stream) {
   {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (auto it = g_grad_ws.begin(); it != g_grad_ws.end();) {
+    for (auto it = g_stream_ws.begin(); it != g_stream_ws.end();) {
       if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
         (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
         if (it->second.first) (void)hipFree(it->second.first);
-        it = g_grad_ws.erase(it);
+        it = g_stream_ws.erase(it);
       } else {
         ++it;
       }

@@ -28,38 +28,6 @@
 
 namespace gev2 {
 
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Buffer resource words matching make_rsrc (raw buffer, 2^31 - 1 bytes).
-__device__ __forceinline__ i32x4_t rsrc_words(const void* base) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4_t r;
-  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
-  r[2] = 0x7fffffff;
-  r[3] = 0x00020000;
-  return r;
-}
-
-// 16 bytes per lane from rsrc + voff + soff into LDS [lds_addr + 16 * lane].
-// M0 is reserved to the compiler, which warns about the clobber; nothing else
-// in these kernels uses M0 (LDS instructions on gfx9+ do not read it), which
-// the generated code shows, so the value set here is only read by this load.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const i32x4_t& rsrc, int voff, int soff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
-}
-
 // Chunk swizzle of K rows.  BK = 64: 8 chunks per 128-byte row, the tile
 // kernel's swz().  BK = 32: 4 chunks per 64-byte row; ((row >> 1) ^ (row >> 3))
 // & 3 gives the rows of equal parity in any aligned 8 (and the rows of equal

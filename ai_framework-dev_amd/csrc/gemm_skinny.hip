@@ -16,6 +16,8 @@
 //     uses v_dot2_f32_{bf16,f16} on W row pairs; fp32 uses FMA;
 //   - the 128 row lanes are summed by a fixed shuffle tree and a fixed-order
 //     LDS pass (deterministic), then bias / activation / Z / Y.
+#include <cstdlib>
+
 #include "gev2_device.hpp"
 #include "gev2_kernels.hpp"
 
@@ -35,7 +37,6 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   }
 }
 
-constexpr int kOobOffsetSk = static_cast<int>(0x80000000u);
 constexpr int kSkThreads = 256;
 constexpr int kSkRowLanes = kSkThreads / 2;   // lane pairs
 
@@ -88,7 +89,7 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(SkinnyArgs p) {
 #pragma unroll
       for (int r = 0; r < RSTEP; ++r) {
         const int k = kc0 + (rl + kSkRowLanes * i) * RSTEP + r;
-        const int off = (nok && k < p.K) ? static_cast<int>(((int64_t)k * p.ldb + n) * sizeof(T)) : kOobOffsetSk;
+        const int off = (nok && k < p.K) ? static_cast<int>(((int64_t)k * p.ldb + n) * sizeof(T)) : kOobOffset;
         w[i][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rW, off, 0, 0));
       }
     // stage X[:, kc0 : kc0 + kSkChunk) (zero beyond M and K); with x_vec each
@@ -194,8 +195,227 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(SkinnyArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 16-bit skinny forward: split-K over 256 x 256 blocks of W, streamed straight
+// into LDS, v_mfma_f32_16x16x32, fixed-order reduction in a second pass.
+//
+// Reading W in 32-byte pieces per row (one column slab per workgroup over all
+// of K) caps a 32 MB read near 2.3 TB/s on this part, while 512-byte row
+// segments reach ~4.9 TB/s.  So a workgroup owns a block of 256 rows x 256
+// columns (512 bytes of each row, 128 KB), and wave w takes its 64 columns
+// over all 256 rows: each wave loads, transposes and multiplies only its own
+// data, with no cross-wave reduction.  Per wave, 32 buffer_load ... lds of
+// 1 KB (8 rows x 128 bytes) are all in flight from the start; the rows sit in
+// LDS with the 32-byte block index XOR-swizzled by (k & 3), so the transpose
+// reads of a 16-lane group (4 rows x 32 bytes) hit distinct banks.  The X
+// block (16 rows, rows past M zero, as 8-k blocks of 16 rows x 16 bytes) is
+// loaded the same way, a quarter per wave.  The K loop waits for the first
+// 128 rows, runs their 4 k-steps, then waits for the rest.
+//   One K block: the workgroup applies bias / activation / Z / Y itself.
+//   Otherwise it writes fp32 partials in the MFMA result layout (16 bytes per
+//   lane, only lanes holding rows < M) and skinny_reduce_kernel adds the K
+//   blocks in order and applies the epilogue.
+// ---------------------------------------------------------------------------
 template <typename T>
-static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
+__device__ __forceinline__ f32x4_t mfma16(const u32x4& a, const u32x4& b, const f32x4_t& c) {
+  if constexpr (__is_same(T, __bf16))
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+}
+
+constexpr int kSplitCols = 256;   // W columns per workgroup (64 per wave)
+constexpr int kSplitRows = 256;   // W rows (K) per workgroup
+
+template <typename T>
+__device__ __forceinline__ void skinny_out(const SkinnyArgs& p, int m, int n, float acc) {
+  T* Y = reinterpret_cast<T*>(p.D);
+  T* Zo = reinterpret_cast<T*>(p.Zo);
+  float pre = p.alpha == 1.f ? acc : p.alpha * acc;
+  if (p.bias) pre += load_bias(p.bias, p.bias_kind, m, n);
+  if (Zo) Elem<T>::store1(Zo + (int64_t)m * p.ldzo + n, pre);
+  Elem<T>::store1(Y + (int64_t)m * p.ldd + n, act_fwd(pre, p.act, p.slope));
+}
+
+// partial of (split, 16-column tile, lane): lanes 0 .. 16*MQ-1 (rows < 4*MQ)
+__device__ __forceinline__ int64_t skinny_part_index(int split, int ntile, int tile, int lane, int mq) {
+  return ((int64_t)split * ntile + tile) * (16 * mq) + lane;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
+  constexpr int RB = 128;                            // bytes per W row per wave (64 columns)
+  constexpr int NWL = kSplitRows * RB / 1024;        // W loads per wave (32)
+  constexpr int WBYTES = kSplitRows * RB;            // 32 KB per wave
+  constexpr int XBYTES = kSplitRows / 8 * 256;       // 8 KB: 32 k-blocks x 16 rows x 16 B
+  __shared__ __attribute__((aligned(1024))) char lds[4 * WBYTES + XBYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slab = blockIdx.x % nslab, split = blockIdx.x / nslab;
+  const int c0 = slab * kSplitCols + wave * 64;      // this wave's first column
+  const int k0 = split * kSplitRows;
+  char* wl = lds + wave * WBYTES;
+  char* xl = lds + 4 * WBYTES;
+
+  // X: load i (of 8, two per wave) fills k-blocks 4i .. 4i+3: lane -> block
+  // 4i + lane/16, row m = lane % 16
+  const i32x4_t rX = rsrc_words(p.A);
+  {
+    const int m = lane & 15;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * wave + ii;
+      const int k = k0 + 8 * (4 * i + (lane >> 4));
+      const int off = (m < p.M && k < p.K) ? static_cast<int>(((int64_t)m * p.lda + k) * sizeof(T)) : kOobOffset;
+      dma16(rX, off, 0, lds_addr(xl) + i * 1024);
+    }
+  }
+  // W: load j fills rows 8j .. 8j+7 of this wave's 128-byte rows; the lane's
+  // 16 bytes hold logical 32-byte block (physical ^ (row & 3))
+  const i32x4_t rW = rsrc_words(p.B);
+  {
+    const int rsub = lane >> 3, pb = (lane & 7) >> 1, half = lane & 1;
+    const uint32_t wl_addr = lds_addr(wl);
+#pragma unroll
+    for (int j = 0; j < NWL; ++j) {
+      const int row = 8 * j + rsub;
+      const int col = c0 + ((pb ^ (row & 3)) << 4) + half * 8;
+      const int k = k0 + row;
+      const int off = (k < p.K && col < p.N) ? static_cast<int>(((int64_t)k * p.ldb + col) * sizeof(T)) : kOobOffset;
+      dma16(rW, off, 0, wl_addr + j * 1024);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (NWL & 0xf) | ((NWL >> 4) << 14));   // vmcnt(NWL): X loads done
+  __syncthreads();                                                          // X block complete
+
+  f32x4_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // transpose reads: lane 16g + 4e + c addresses columns 16t + 4c.. of row
+  // 32s + 8g + 4h + e
+  const int g = lane >> 4, e = (lane >> 2) & 3, cq = lane & 3;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    // rows [128 half, 128 half + 128) are W loads [16 half, 16 half + 16)
+    if (half == 0) __builtin_amdgcn_s_waitcnt(0x3f70 | (NWL / 2 & 0xf) | ((NWL / 2) >> 4 << 14));
+    else __builtin_amdgcn_s_waitcnt(0x3f70);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const int s = 4 * half + ss;
+      const u32x4 xa = *reinterpret_cast<const u32x4*>(xl + s * 1024 + lane * 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        u32x4 wf;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k = 32 * s + 8 * g + 4 * h + e;
+          const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4_t*)(wl + k * RB + ((t ^ (k & 3)) << 5) + cq * 8));
+          const u32x2 w2 = __builtin_bit_cast(u32x2, v);
+          wf[2 * h] = w2[0];
+          wf[2 * h + 1] = w2[1];
+        }
+        acc[t] = mfma16<T>(xa, wf, acc[t]);
+      }
+    }
+  }
+
+  // D[m][n]: n = c0 + 16 t + lane % 16, m = 4 (lane / 16) + r
+  const int nsplit = gridDim.x / nslab;
+  if (nsplit == 1) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int n = c0 + 16 * t + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * (lane >> 4) + r;
+        if (m < p.M && n < p.N) skinny_out<T>(p, m, n, acc[t][r]);
+      }
+    }
+  } else {
+    const int mq = (p.M + 3) / 4;
+    if (lane < 16 * mq) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        part[skinny_part_index(split, nslab * 16, slab * 16 + wave * 4 + t, lane, mq)] = acc[t];
+    }
+  }
+}
+
+// Y = act(alpha * sum_s part[s] + bias), K blocks added in order s = 0, 1, ...
+// One thread per (16-column tile, lane) of the MFMA result layout, i.e. per 4
+// rows of one column; up to 16 partial vectors are in flight at once.
+constexpr int kReduceThreads = 64;
+
+template <typename T>
+__global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArgs p, const f32x4_t* part, int nsplit,
+                                                                       int ntile) {
+  const int mq = (p.M + 3) / 4;
+  const int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
+  const int64_t per_split = (int64_t)ntile * 16 * mq;
+  if (i >= per_split) return;
+  const int tile = static_cast<int>(i / (16 * mq)), lane = static_cast<int>(i % (16 * mq));
+  f32x4_t sum = part[i];
+  for (int s0 = 1; s0 < nsplit; s0 += 16) {
+    f32x4_t v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      v[u] = s0 + u < nsplit ? part[(s0 + u) * per_split + i] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (s0 + u < nsplit)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] += v[u][r];
+  }
+  const int n = tile * 16 + (lane & 15);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * (lane >> 4) + r;
+    if (m < p.M && n < p.N) skinny_out<T>(p, m, n, sum[r]);
+  }
+}
+
+template <typename T>
+static hipError_t launch_skinny_split(const SkinnyArgs& a, float* part, hipStream_t s) {
+  const int nslab = (a.N + kSplitCols - 1) / kSplitCols;
+  const int nsplit = (a.K + kSplitRows - 1) / kSplitRows;
+  f32x4_t* pv = reinterpret_cast<f32x4_t*>(part);
+  hipLaunchKernelGGL((gemm_skinny_split_kernel<T>), dim3(nslab * nsplit), dim3(256), 0, s, a, pv, nslab);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nsplit == 1) return e;
+  const int64_t threads = (int64_t)nslab * 16 * 16 * ((a.M + 3) / 4);
+  hipLaunchKernelGGL((skinny_reduce_kernel<T>), dim3(static_cast<unsigned>((threads + kReduceThreads - 1) / kReduceThreads)),
+                     dim3(kReduceThreads), 0, s, a, pv, nsplit, nslab * 16);
+  return hipGetLastError();
+}
+
+// nsplit x nslab x 16 tiles x 16*ceil(M/4) lanes x 16 bytes
+int64_t skinny_split_workspace_bytes(int M, int N, int K) {
+  const int64_t nsplit = (K + kSplitRows - 1) / kSplitRows;
+  const int64_t nslab = (N + kSplitCols - 1) / kSplitCols;
+  return nsplit > 1 ? nsplit * nslab * 16 * 16 * ((M + 3) / 4) * 16 : 0;
+}
+
+// The split kernel takes 16-bit data with 16-byte aligned X rows spanning
+// < 2^31 bytes (x_vec == 2) and M <= 16; GEV2_SKINNY_DOT=1 selects the
+// dot-product kernel below instead (comparison runs).
+bool skinny_split_eligible(const SkinnyArgs& a) {
+  if (a.x_vec != 2 || a.M > 16) return false;
+  const char* v = std::getenv("GEV2_SKINNY_DOT");
+  return !(v && v[0] == '1');
+}
+
+template <typename T>
+static hipError_t launch_skinny_t(const SkinnyArgs& a, float* part, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    // x_vec == 2: X rows are 16-byte aligned and span < 2^31 bytes (host)
+    if (skinny_split_eligible(a)) return launch_skinny_split<T>(a, part, s);
+  }
   constexpr int COLS = sk_cols<T>();
   dim3 grid((a.N + COLS - 1) / COLS);
   if (a.M <= 8)
@@ -205,11 +425,11 @@ static hipError_t launch_skinny_t(const SkinnyArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_skinny(int dtype, const SkinnyArgs& a, hipStream_t s) {
+hipError_t launch_skinny(int dtype, const SkinnyArgs& a, float* part, hipStream_t s) {
   switch (dtype) {
-    case kF32: return launch_skinny_t<float>(a, s);
-    case kBF16: return launch_skinny_t<__bf16>(a, s);
-    case kF16: return launch_skinny_t<_Float16>(a, s);
+    case kF32: return launch_skinny_t<float>(a, part, s);
+    case kBF16: return launch_skinny_t<__bf16>(a, part, s);
+    case kF16: return launch_skinny_t<_Float16>(a, part, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -379,7 +379,6 @@ gemm_tile_kernel(TileArgs p) {
 //     1 and 2 into the other LDS buffer; one barrier per K tile;
 //   - the backward's epilogue (PRO != 0) is compiled for act = none only.
 // ---------------------------------------------------------------------------
-constexpr int kOobOffset = static_cast<int>(0x80000000u);
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   // range 2^31 - 1 bytes: every valid offset is below it (checked by the

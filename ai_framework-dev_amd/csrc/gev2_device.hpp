@@ -24,6 +24,46 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // one 16-byte chunk
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// ---------------------------------------------------------------------------
+// Raw buffer addressing and direct-to-LDS loads (buffer_load ... lds)
+// ---------------------------------------------------------------------------
+// Byte offset that lies outside every buffer resource made here (their range
+// is 2^31 - 1 bytes): loads from it return zero, stores to it are dropped.
+constexpr int kOobOffset = static_cast<int>(0x80000000u);
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource words of a raw buffer of 2^31 - 1 bytes at `base`: an
+// offset at or past 2^31 - 1 (kOobOffset) reads as zero.
+__device__ __forceinline__ i32x4_t rsrc_words(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));
+  r[2] = 0x7fffffff;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from rsrc + voff + soff into LDS [lds_addr + 16 * lane].
+// M0 is reserved to the compiler, which warns about the clobber; nothing else
+// in these kernels uses M0 (LDS instructions on gfx9+ do not read it), which
+// the generated code shows, so the value set here is only read by this load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const i32x4_t& rsrc, int voff, int soff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_addr)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
 constexpr float kGeluC = 0.7978845608f;
 constexpr float kGeluK1 = 0.044715f;
 

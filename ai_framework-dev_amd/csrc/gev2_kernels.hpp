@@ -30,8 +30,10 @@ struct TileArgs {
   int store_vec;         // D/Zo rows: 0 scalar, 1 4-wide vector stores, 2 16-byte row segments (16-bit)
 };
 
-// Skinny forward (M <= kSkinnyMaxM): one workgroup per 32-byte column slab of
-// W over all of K (no cross-workgroup reduction, no workspace).
+// Skinny forward (M <= kSkinnyMaxM): for 16-bit data a split-K kernel over
+// 256 x 256 blocks of W with fp32 partials in a workspace and a fixed-order
+// reduction pass; otherwise one workgroup per 32-byte column slab of W over
+// all of K (no cross-workgroup reduction, no workspace).
 constexpr int kSkinnyMaxM = 16;
 struct SkinnyArgs {
   const void* A; const void* B; void* D; void* Zo;
@@ -40,7 +42,7 @@ struct SkinnyArgs {
   int M, N, K;
   int act, bias_kind;
   float slope, alpha;
-  int x_vec;             // X rows 16-byte aligned with K a multiple of the chunk
+  int x_vec;             // 1: X rows 16-byte aligned, K % chunk == 0; 2: also spans < 2^31 bytes
 };
 
 // Element-wise gZ = gY * act'(Z) (optionally scaled by beta) -> out, and
@@ -91,7 +93,10 @@ hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const T
 hipError_t launch_dl_bf16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
 hipError_t launch_dl_f16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
 bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a);
-hipError_t launch_skinny(int dtype, const SkinnyArgs& a, hipStream_t s);
+// part: fp32 partial sums for the split-K 16-bit kernel (skinny_split_workspace_bytes)
+hipError_t launch_skinny(int dtype, const SkinnyArgs& a, float* part, hipStream_t s);
+bool skinny_split_eligible(const SkinnyArgs& a);
+int64_t skinny_split_workspace_bytes(int M, int N, int K);
 hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const GradArgs& a, int batch, hipStream_t s);
 

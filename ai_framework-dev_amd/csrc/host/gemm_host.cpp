@@ -177,6 +177,10 @@ static Status forward_impl(const Tensor& A, const Tensor& B, const Tensor* Bias,
   d.stride_bias = bt.stride_bias;
   d.Y = Y.data; d.ldy = ldd; d.stride_y = bt.stride_y;
   d.Z = want_z ? Z_saved->data : nullptr; d.ldz = ldz; d.stride_z = bt.stride_z;
+  if (ws && ws->scratch) {   // split-K partials of skinny problems (gev2_gemm_fwd_workspace_size)
+    d.workspace = ws->scratch;
+    d.workspace_bytes = static_cast<int64_t>(ws->scratch_bytes);
+  }
   return from_abi(gev2_gemm_fwd(&d, stream));
 }
 

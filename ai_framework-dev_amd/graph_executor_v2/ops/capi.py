@@ -20,7 +20,7 @@ ACT = {"none": 0, "relu": 1, "leakyrelu": 2, "leaky_relu": 2, "lrelu": 2, "gelu"
 BIAS_NONE, BIAS_SCALAR, BIAS_PERM, BIAS_PERN = 0, 1, 2, 3
 
 EXPORTED = [
-    "gev2_gemm_fwd", "gev2_gemm_bwd", "gev2_gemm_fwd_repeat", "gev2_gemm_bwd_repeat", "gev2_abi_version", "gev2_status_string",
+    "gev2_gemm_fwd", "gev2_gemm_bwd", "gev2_gemm_fwd_workspace_size", "gev2_gemm_fwd_repeat", "gev2_gemm_bwd_repeat", "gev2_abi_version", "gev2_status_string",
     "gev2_last_error", "gev2_last_path", "gev2_device_count", "gev2_set_device",
     "gev2_get_device", "gev2_device_info", "gev2_malloc", "gev2_free", "gev2_memcpy_htod",
     "gev2_memcpy_dtoh", "gev2_memcpy_dtod_async", "gev2_memset", "gev2_stream_create",
@@ -41,6 +41,7 @@ class FwdDesc(ctypes.Structure):
         ("bias", ctypes.c_void_p), ("stride_bias", ctypes.c_int64),
         ("Y", ctypes.c_void_p), ("ldy", ctypes.c_int64), ("stride_y", ctypes.c_int64),
         ("Z", ctypes.c_void_p), ("ldz", ctypes.c_int64), ("stride_z", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -83,6 +84,8 @@ def lib() -> ctypes.CDLL:
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     L.gev2_gemm_fwd.argtypes = [ctypes.POINTER(FwdDesc), vp]
     L.gev2_gemm_bwd.argtypes = [ctypes.POINTER(BwdDesc), vp]
+    L.gev2_gemm_fwd_workspace_size.argtypes = [ctypes.POINTER(FwdDesc)]
+    L.gev2_gemm_fwd_workspace_size.restype = i64
     L.gev2_gemm_fwd_repeat.argtypes = [ctypes.POINTER(FwdDesc), i32, i32, vp]
     L.gev2_gemm_bwd_repeat.argtypes = [ctypes.POINTER(BwdDesc), i32, i32, vp]
     for f in ("gev2_status_string",):
@@ -237,7 +240,8 @@ def fwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, Y: int,
              leaky_slope: float = 0.01, alpha: float = 1.0, trans_a: bool = False,
              trans_b: bool = False, batch: int = 1, lda: int = 0, ldb: int = 0, ldy: int = 0,
              ldz: int = 0, stride_a: int = 0, stride_b: int = 0, stride_y: int = 0,
-             stride_z: int = 0, stride_bias: int = 0) -> FwdDesc:
+             stride_z: int = 0, stride_bias: int = 0, workspace: int = 0,
+             workspace_bytes: int = 0) -> FwdDesc:
     d = FwdDesc()
     d.dtype, d.act, d.bias_kind = dtype, ACT[act] if isinstance(act, str) else int(act), bias_kind
     d.trans_a, d.trans_b = int(trans_a), int(trans_b)
@@ -248,7 +252,17 @@ def fwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, Y: int,
     d.bias, d.stride_bias = bias or None, stride_bias
     d.Y, d.ldy, d.stride_y = Y or None, ldy, stride_y
     d.Z, d.ldz, d.stride_z = Z or None, ldz, stride_z
+    d.workspace, d.workspace_bytes = workspace or None, workspace_bytes
     return d
+
+
+def fwd_workspace_size(**kw) -> int:
+    """Scratch bytes gev2_gemm_fwd needs for these arguments (0: none)."""
+    d = fwd_desc(**kw)
+    n = lib().gev2_gemm_fwd_workspace_size(ctypes.byref(d))
+    if n < 0:
+        raise GemmError(1, "gev2_gemm_fwd_workspace_size", lib().gev2_last_error().decode())
+    return n
 
 
 def bwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, gY: int, Z: int,

@@ -242,7 +242,8 @@ def conv_cfg(ctx, dtype, iters):
 
 
 def skinny_cfg(ctx, iters, sets=10):
-    """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL."""
+    """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL.
+    The split-K partials go to a caller workspace (gev2_gemm_fwd_workspace_size)."""
     capi = ctx.capi
     M, N, K = 8, 4096, 4096
     g = np.random.default_rng(66)
@@ -251,8 +252,10 @@ def skinny_cfg(ctx, iters, sets=10):
     pb = ctx.put(normal(g, (N,), 0.02))
     Ws = [ctx.put(capi.to_storage(normal(g, (K, N), 1 / np.sqrt(K)), capi.BF16)) for _ in range(sets)]
     pY = ctx.empty(M * N * 2)
-    fds = [capi.fwd_desc(dtype=capi.BF16, M=M, N=N, K=K, A=pX, B=w, Y=pY, bias=pb,
-                         bias_kind=capi.BIAS_PERN, act="none") for w in Ws]
+    kw = dict(dtype=capi.BF16, M=M, N=N, K=K, A=pX, Y=pY, bias=pb, bias_kind=capi.BIAS_PERN, act="none")
+    need = capi.fwd_workspace_size(B=Ws[0], **kw)
+    ws = ctx.empty(max(need, 256))
+    fds = [capi.fwd_desc(B=w, workspace=ws, workspace_bytes=need, **kw) for w in Ws]
     capi.gemm_fwd_repeat(fds, 1, ctx.stream.ptr)
     path = capi.last_path()
     ms = ctx.time_repeat(fds, iters, "fwd")

@@ -24,9 +24,11 @@
  *     GEV2_HIP_ERROR (130) is the reference's CUDA_ERROR slot.  The functions
  *     never throw; gev2_last_error() gives a message for the calling thread.
  *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = null stream).
- *   - gev2_gemm_fwd never allocates device memory.  gev2_gemm_bwd allocates
- *     only when it materialises dY' and no large enough `workspace` is given
- *     (see gev2_gemm_bwd_desc).
+ *   - Device memory is allocated only for scratch that the caller did not
+ *     pass in `workspace`: the forward's split-K partial sums for skinny
+ *     16-bit problems (gev2_gemm_fwd_workspace_size gives the size, 0 for all
+ *     other problems) and the backward's materialised dY'.  Such a buffer is
+ *     allocated once per (device, stream) and kept until gev2_stream_destroy.
  */
 #ifndef GEV2_GEMM_H_
 #define GEV2_GEMM_H_
@@ -38,7 +40,7 @@
 extern "C" {
 #endif
 
-#define GEV2_ABI_VERSION 2
+#define GEV2_ABI_VERSION 3
 
 /* Status (values of ai::cuda::shim::Status, ai_status.hpp:14-43) */
 enum {
@@ -75,6 +77,10 @@ enum { GEV2_BIAS_NONE = 0, GEV2_BIAS_SCALAR = 1, GEV2_BIAS_PER_M = 2, GEV2_BIAS_
  * bias may be NULL or bias_kind NONE; PerN indexes bias[n], PerM bias[m].
  * Replaces GemmCudaLaunch (launcher.cu:147-274), which only has batch = 1,
  * alpha = 1 and no transposes (it returns TransposeNotSupported for them).
+ * workspace: optional scratch (256-byte aligned) of at least
+ * gev2_gemm_fwd_workspace_size(desc) bytes; NULL or too small makes the
+ * library use its own per-(device, stream) buffer.  Plays the role of the
+ * reference's GemmWorkspace (gemm/api.hpp:97-104, GemmCudaLaunch's ws).
  */
 typedef struct gev2_gemm_fwd_desc {
   int32_t dtype;
@@ -91,6 +97,7 @@ typedef struct gev2_gemm_fwd_desc {
   const float* bias; int64_t stride_bias;
   void* Y;           int64_t ldy, stride_y;
   void* Z;           int64_t ldz, stride_z;
+  void* workspace;   int64_t workspace_bytes;
 } gev2_gemm_fwd_desc;
 
 /*
@@ -134,6 +141,9 @@ typedef struct gev2_gemm_bwd_desc {
 } gev2_gemm_bwd_desc;
 
 int gev2_gemm_fwd(const gev2_gemm_fwd_desc* desc, void* stream);
+/* Scratch bytes gev2_gemm_fwd uses for `desc` (0: none); -1 for an invalid
+ * descriptor.  No counterpart in the reference (its forward needs none). */
+int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* desc);
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
 
 /*
@@ -149,7 +159,8 @@ const char* gev2_status_string(int status);
 /* Message for the last failing call on this thread ("" if none). */
 const char* gev2_last_error(void);
 /* Name of the kernel family the last gev2_gemm_fwd on this thread used
- * ("tile:<cfg>", "skinny"), for tests and profiling. */
+ * ("dl:<cfg>", "tile:<cfg>", "skinny:split", "skinny"), for tests and
+ * profiling. */
 const char* gev2_last_path(void);
 
 /*

@@ -18,13 +18,14 @@ def capi():
 
 def test_exports_every_declared_symbol(capi):
     hdr = open(os.path.join(REPO, "include", "gev2_gemm.h")).read()
-    names = set(re.findall(r"^\s*(?:int|const char\*)\s+(gev2_\w+)\s*\(", hdr, re.M))
+    names = set(re.findall(r"^\s*(?:int64_t|int|const char\*)\s+(gev2_\w+)\s*\(", hdr, re.M))
+    assert "gev2_gemm_fwd_workspace_size" in names
     assert "gev2_gemm_fwd" in names and "gev2_gemm_bwd" in names
     L = capi.lib()
     missing = [n for n in sorted(names) if not hasattr(L, n)]
     assert not missing, missing
     assert set(names) <= set(capi.EXPORTED)
-    assert L.gev2_abi_version() == 2
+    assert L.gev2_abi_version() == 3
 
 
 def test_status_strings(capi):
@@ -85,3 +86,28 @@ def test_storage_roundtrip(capi):
     for dt in (capi.F32, capi.F16, capi.BF16):
         s = capi.to_storage(x, dt)
         assert np.array_equal(capi.from_storage(s, dt), O.round_to(x, dt))
+
+
+def _ws_size(capi, **kw):
+    import ctypes
+    d = capi.FwdDesc()
+    d.dtype, d.M, d.N, d.K, d.batch, d.alpha = 2, 8, 4096, 4096, 1, 1.0
+    d.A, d.B, d.Y = 1 << 20, 1 << 28, 1 << 30     # 16-byte aligned, never dereferenced
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return capi.lib().gev2_gemm_fwd_workspace_size(ctypes.byref(d))
+
+
+def test_forward_workspace_size(capi):
+    """Split-K partials of skinny 16-bit problems: K blocks of 256 x 256-column slabs x
+    16 tiles x 16*ceil(M/4) lanes x 16 bytes (= ceil(K/256) * M * N * 4 for M % 4 == 0,
+    N % 256 == 0); none for one K block, fp32 data, the tile path, or empty problems;
+    -1 for a bad descriptor."""
+    assert _ws_size(capi) == 16 * 8 * 4096 * 4
+    assert _ws_size(capi, K=4096 + 8) == 17 * 8 * 4096 * 4
+    assert _ws_size(capi, M=5, N=520) == 16 * 3 * 16 * 16 * 2 * 16
+    assert _ws_size(capi, K=256) == 0                 # one K block: epilogue in the kernel
+    assert _ws_size(capi, dtype=0) == 0               # fp32: dot-product kernel, no workspace
+    assert _ws_size(capi, M=64) == 0                  # tile path
+    assert _ws_size(capi, M=0) == 0
+    assert _ws_size(capi, dtype=7) == -1

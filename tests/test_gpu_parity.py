@@ -70,7 +70,7 @@ def test_forward_shapes(gpu, dtype, shape):
     bias = BIASES[(i + 2 * dtype) % len(BIASES)]
     path = _check_fwd(gpu, M, N, K, dtype, act, bias, seed=1000 + 10 * i + dtype)
     if M <= 16 and K >= 64:
-        assert path == "skinny"
+        assert path.startswith("skinny")
     elif (K * (4 if dtype == F32 else 2)) % 16:
         assert path.endswith("scalar")
 
@@ -334,12 +334,13 @@ def test_backward_both_dy_paths(gpu, fused, monkeypatch):
 def test_skinny_full_size(gpu):
     """BASELINE config 5b: M=8, N=K=4096, bf16, bias, through the skinny kernel."""
     path = _check_fwd(gpu, 8, 4096, 4096, BF16, "none", O.BIAS_PERN, seed=55)
-    assert path == "skinny"
+    assert path == "skinny:split"
 
 
 def test_skinny_repeat_calls(gpu):
-    """Repeated skinny calls (X chunks staged per call in LDS) stay correct; K = 2048 + 640
-    also covers a partial second K chunk."""
+    """Repeated skinny calls stay correct (the split-K partials in the per-stream
+    workspace are rewritten by every call); K = 2048 + 640 also covers a partial
+    last K block."""
     for i in range(3):
         _check_fwd(gpu, 4, 384, 2048, BF16, "relu", O.BIAS_PERN, seed=60 + i)
     _check_fwd(gpu, 16, 264, 2688, F32, "gelu", O.BIAS_PERM, seed=64)

@@ -90,3 +90,55 @@ def test_dl_bias_kinds_exact(gpu, monkeypatch, bias_kind, dtype):
     assert path == "dl:256x256", path
     assert np.array_equal(Z, Zr)
     assert np.array_equal(Y, Yr)
+
+
+# Skinny forward (M <= 16): the split-K MFMA kernel (one K block when K <= 256,
+# otherwise fp32 partials in the workspace plus the fixed-order reduction),
+# and the dot-product kernel it replaces for 16-bit data (GEV2_SKINNY_DOT=1).
+SKINNY = [(8, 4096, 4096), (13, 264, 328), (1, 72, 64), (16, 1000, 1032), (5, 136, 2056), (3, 520, 256)]
+
+
+@pytest.mark.parametrize("variant", ["0", "1"], ids=["dl", "dot2"])
+@pytest.mark.parametrize("shape", SKINNY, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=lambda d: DT_NAMES[d])
+def test_skinny_variants_exact(gpu, monkeypatch, variant, shape, dtype):
+    capi = gpu
+    monkeypatch.setenv("GEV2_SKINNY_DOT", variant)
+    M, N, K = shape
+    Y, Z, Yr, Zr, path = _run(capi, "NN", M, N, K, 0, dtype, O.BIAS_PERN, "relu", seed=M + N)
+    assert path == ("skinny" if variant == "1" else "skinny:split"), path
+    assert np.array_equal(Z, Zr), f"Z {shape}"
+    assert np.array_equal(Y, Yr), f"Y {shape}"
+
+
+def test_skinny_explicit_workspace(gpu):
+    """A caller-provided workspace (gev2_gemm_fwd_workspace_size bytes) gives the same
+    bits as the library's per-stream buffer, and two problems in a row that share it
+    (the second smaller) are both right."""
+    capi = gpu
+    g = np.random.default_rng(21)
+    dev = Dev(capi)
+    try:
+        for (M, N, K) in [(8, 4096, 4096), (3, 520, 1032)]:
+            X, W = _ints(g, (M, K)), _ints(g, (K, N))
+            b = _ints(g, (N,), -3, 3)
+            pX, pW, pb = dev.put(capi.to_storage(X, BF16)), dev.put(capi.to_storage(W, BF16)), dev.put(b)
+            outs = []
+            for own in (False, True):
+                pY = dev.empty(M * N * 2)
+                kw = dict(dtype=BF16, M=M, N=N, K=K, A=pX, B=pW, Y=pY, bias=pb, bias_kind=O.BIAS_PERN,
+                          act="relu")
+                need = capi.fwd_workspace_size(**kw)
+                # K blocks x 256-column slabs x 16 tiles x 16*ceil(M/4) lanes x 16 bytes
+                assert need == -(-K // 256) * -(-N // 256) * 16 * 16 * -(-M // 4) * 16
+                if own:
+                    kw.update(workspace=dev.empty(need), workspace_bytes=need)
+                capi.gemm_fwd(**kw)
+                assert capi.last_path() == "skinny:split"
+                capi.synchronize()
+                outs.append(dev.get(pY, (M, N), BF16))
+            Y64, _ = O.gemm_forward(X, W, b, O.BIAS_PERN, "relu")
+            assert np.array_equal(outs[0], rounded(Y64, BF16))
+            assert np.array_equal(outs[1], outs[0])
+    finally:
+        dev.close()
