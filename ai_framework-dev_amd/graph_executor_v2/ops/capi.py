@@ -26,7 +26,7 @@ EXPORTED = [
     "gev2_memcpy_dtoh", "gev2_memcpy_dtod_async", "gev2_memset", "gev2_stream_create",
     "gev2_stream_destroy", "gev2_stream_synchronize", "gev2_device_synchronize",
     "gev2_event_create", "gev2_event_destroy", "gev2_event_record", "gev2_event_synchronize",
-    "gev2_event_elapsed_ms",
+    "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16",
 ]
 
 
@@ -112,6 +112,7 @@ def lib() -> ctypes.CDLL:
     L.gev2_event_record.argtypes = [vp, vp]
     L.gev2_event_synchronize.argtypes = [vp]
     L.gev2_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+    L.gev2_probe_mfma_bf16.argtypes = [i32, i32, vp]
     _lib = L
     return L
 

@@ -7,7 +7,9 @@ in HBM.  value = 6*M*N*K / step time (TFLOP/s).
 
 roofline: the forward GEMM+bias+ReLU kernel timed alone with HIP events on the
 stream it is launched on; achieved = 2*M*N*K / average launch time, against the
-dense bf16 MFMA peak (2516.6 TFLOP/s).
+dense bf16 MFMA peak (2516.6 TFLOP/s).  Beside it, the sustained rate of
+back-to-back bf16 MFMAs with zero and with random operands (gev2_probe_mfma_bf16)
+shows how far below the published peak the matrix cores run on real data.
 
 cpu_baseline: the reference's NumPy path (smoke_gemm_binding.py:84-123,
 restated in oracle/gemm_oracle.py) in fp32 on the host's cores, on a bounded
@@ -297,7 +299,7 @@ def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=40):
 def measured_traffic():
     """HBM bytes per forward launch, as recorded from the rocprofv3 FETCH_SIZE /
     WRITE_SIZE runs (scaled by a copy of known size) in profiles/; None if absent."""
-    path = os.path.join(REPO, "profiles", "gemm_pipe_bf16_256x256_nn_4096_traffic.md")
+    path = os.path.join(REPO, "profiles", "gemm_dl_bf16_256x256_nn_4096_traffic.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -307,11 +309,29 @@ def measured_traffic():
     return None
 
 
+def mfma_ceiling(ctx, iters=4096):
+    """Sustained back-to-back bf16 MFMA rate (TFLOP/s) with zero and with random operands
+    (gev2_probe_mfma_bf16): the clock the matrix cores hold depends on the data."""
+    capi = ctx.capi
+    _, cus, _ = capi.device_info(0)
+    flop = cus * 4 * iters * 16 * 32768.0
+    out = {}
+    for name, rnd in (("zero", 0), ("random", 1)):
+        ms = ctx.time_ms(lambda: capi.check(capi.lib().gev2_probe_mfma_bf16(rnd, iters, ctx.stream.ptr),
+                                            "probe"), 10, warmup=2)
+        out[name] = round(flop / (ms * 1e-3) / 1e12, 1)
+    return out
+
+
+def kernel_name(path):
+    return {"dl": "gemm_dl_kernel", "tile": "gemm_pipe_kernel"}.get(path.split(":")[0], path)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the operator's multi-GPU "
-                          "sharding is design-only (see DESIGN.md); run with --gpus 1"}))
+                          "sharding is a design, not code; run with --gpus 1"}))
         return 2
     from graph_executor_v2.ops import capi
     capi.lib()
@@ -352,6 +372,8 @@ def main():
                 r = {k: r[k] for k in ("step_ms", "fwd_ms", "bwd_ms", "tflops_step", "tflops_fwd")}
             extra[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
             print(f"# {key}: {extra[key]}", file=sys.stderr, flush=True)
+    ceiling = mfma_ceiling(ctx)
+    print(f"# mfma probe: {ceiling}", file=sys.stderr, flush=True)
     flop = 2.0 * 4096 ** 3
     achieved = flop / (res["fwd_ms"] * 1e-3) / 1e12
     line = {
@@ -372,8 +394,10 @@ def main():
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4), "traffic": measured_traffic(),
-                     "kernel": "gemm_pipe_kernel (forward, bf16 " + res["path"] + ")",
-                     "flop_per_launch": flop},
+                     "kernel": kernel_name(res["path"]) + " (forward, bf16, " + res["path"] + ")",
+                     "flop_per_launch": flop,
+                     "mfma_probe_tflops": ceiling,
+                     "frac_of_random_operand_probe": round(achieved / ceiling["random"], 4)},
         "extra": extra,
     }
     if not args.no_cpu:

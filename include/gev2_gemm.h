@@ -154,6 +154,16 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
 int gev2_gemm_fwd_repeat(const gev2_gemm_fwd_desc* descs, int n_descs, int reps, void* stream);
 int gev2_gemm_bwd_repeat(const gev2_gemm_bwd_desc* descs, int n_descs, int reps, void* stream);
 
+/*
+ * Measurement helper (no counterpart in the reference): launches one
+ * 256-thread workgroup per compute unit (one wave per SIMD), each wave
+ * issuing iters x 16 independent v_mfma_f32_32x32x16_bf16 on zero
+ * (random_operands = 0) or random bf16 operands; total FLOP =
+ * CUs * 4 * iters * 16 * 32768.  Time it with events on `stream` to get the
+ * sustained MFMA rate for such data.
+ */
+int gev2_probe_mfma_bf16(int random_operands, int iters, void* stream);
+
 int gev2_abi_version(void);
 const char* gev2_status_string(int status);
 /* Message for the last failing call on this thread ("" if none). */
