@@ -230,7 +230,8 @@ PYBIND11_MODULE(_ops_gemm, m) {
       "A"_a, "B"_a, "C"_a = py::none(), "gY"_a, "Z"_a, "gA"_a = py::none(), "gB"_a = py::none(),
       "gC"_a = py::none(), "gBias"_a = py::none(), "attrs"_a, "stream"_a = py::none(), "dZ_ptr"_a,
       "lt_ws_ptr"_a = static_cast<std::uintptr_t>(0), "lt_ws_bytes"_a = static_cast<std::size_t>(0),
-      "Capture-safe backward (this build allocates nothing in any backward; the dZ buffer is not written).");
+      "Capture-safe backward: the dZ buffer (M*N fp32) is the dY' workspace whenever one is needed, so nothing "
+      "is allocated.");
 
   m.def(
       "forward_ex_attrs",
