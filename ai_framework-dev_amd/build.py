@@ -5,6 +5,7 @@ Outputs (next to the Python package, like the reference's CMake output dir
   graph_executor_v2/ops/libgev2.so        HIP kernels + C ABI (include/gev2_gemm.h)
   graph_executor_v2/ops/_ops_common*.so   pybind11: shared shim types
   graph_executor_v2/ops/_ops_gemm*.so     pybind11: the GEMM op surface
+  graph_executor_v2/ops/_ops_conv2d*.so   pybind11: conv2d on the GEMM op
 
 Usage: python ai_framework-dev_amd/build.py [--force] [-j N]
 """
@@ -28,7 +29,7 @@ INCLUDE = os.path.join(REPO, "include")
 HIP_SOURCES = [
     "gemm_tile_f32.hip", "gemm_tile_bf16.hip", "gemm_tile_f16.hip",
     "gemm_dl_bf16.hip", "gemm_dl_f16.hip",
-    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "probe.hip",
+    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "probe.hip",
 ]
 HIP_HEADERS = ["gev2_device.hpp", "gev2_kernels.hpp", "gemm_tile_impl.hpp", "gemm_dl_impl.hpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -42,8 +43,9 @@ HIP_FLAGS = [
 BIND_SOURCES = {
     "_ops_common": ["bindings/ops_common_pybind.cpp"],
     "_ops_gemm": ["bindings/gemm_pybind.cpp", "host/gemm_host.cpp"],
+    "_ops_conv2d": ["bindings/conv2d_pybind.cpp", "host/conv2d_host.cpp"],
 }
-HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp"]
+HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp"]
 
 
 def _newer(target: str, deps: list[str]) -> bool:
@@ -102,7 +104,7 @@ def build_bindings(force: bool, jobs: int) -> list[str]:
                    "-fvisibility=hidden",
                    f"-I{pybind11.get_include()}", f"-I{py_inc}", f"-I{INCLUDE}", f"-I{CSRC}",
                    *paths, "-o", out + ".tmp"]
-            if mod == "_ops_gemm":
+            if mod in ("_ops_gemm", "_ops_conv2d"):
                 cmd += [f"-L{OUT_DIR}", "-lgev2", "-Wl,-rpath,$ORIGIN"]
             cmds.append((cmd, out))
 

@@ -1,0 +1,307 @@
+// 2-D convolution (NCHW, groups = 1) on the batched GEMM: the conv2d launcher
+// of graph_executor_v2 (backends/cuda/ops/conv2d/launcher.cu:106-459,
+// kernels.cu:12-175) rebuilt around the operator.
+//
+// Forward, per chunk of images:
+//   im2col into Col^T [K, Ho*Wo] per image, K = Cin*Kh*Kw ordered
+//   (c*Kh + kh)*Kw + kw (kernels.cu:12-45), then ONE batched GEMM
+//     Y_n [Cout, Ho*Wo] = W [Cout, K] . Col^T_n  (+ bias per row, act, Z)
+//   whose output rows are already the NCHW planes: the OIHW weight tensor is
+//   the [Cout, K] operand as it lies in memory, so there is no weight packing
+//   and no output transpose (the reference packs W, runs one GEMM per image
+//   into [HWo, Cout] rows and transposes each result).
+// Backward, per chunk of images (as many as the workspaces hold): im2col,
+//   then ONE batched operator backward with A = W (slice stride 0),
+//   B = Col^T_n, gY = dY_n, Z = Z_n, giving per image dW_n = dY'_n Col_n (gA),
+//   the input-gradient columns W^T dY'_n (gB, [K, HWo]) and dB_n (PerM gBias).
+//   dW and dB are summed over images in fp32 in image order, and col2im
+//   gathers each input element's columns in a fixed (kh, kw) order, so the
+//   results do not depend on the chunk size.  (The reference runs one GEMM
+//   backward per image and zero-fills the bias gradient inside each, so its dB
+//   holds the last image only.)
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "../../include/gev2_gemm.h"
+#include "gev2_device.hpp"
+
+namespace gev2 {
+
+struct ConvGeom {
+  int Cin, H, W, Kh, Kw, sh, sw, ph, pw, dh, dw, Ho, Wo;
+};
+
+// col[(img*K + k) * HWo + hw] = X[img][c][h_out*sh - ph + kh*dh][w_out*sw - pw + kw*dw] (0 outside);
+// one block per (row, 256 output positions), consecutive threads on consecutive hw
+template <typename T>
+__global__ void __launch_bounds__(256) im2col_t_kernel(const T* __restrict__ X, T* __restrict__ col, ConvGeom g,
+                                                       int hw_blocks) {
+  const int HWo = g.Ho * g.Wo;
+  const int K = g.Cin * g.Kh * g.Kw;
+  const int64_t row = blockIdx.x / hw_blocks;       // img*K + k
+  const int hw = static_cast<int>(blockIdx.x % hw_blocks) * 256 + threadIdx.x;
+  if (hw >= HWo) return;
+  const int img = static_cast<int>(row / K), k = static_cast<int>(row % K);
+  const int kw = k % g.Kw, kh = (k / g.Kw) % g.Kh, c = k / (g.Kw * g.Kh);
+  const int ho = hw / g.Wo, wo = hw % g.Wo;
+  const int hi = ho * g.sh - g.ph + kh * g.dh, wi = wo * g.sw - g.pw + kw * g.dw;
+  T v{};
+  if (static_cast<unsigned>(hi) < static_cast<unsigned>(g.H) && static_cast<unsigned>(wi) < static_cast<unsigned>(g.W))
+    v = X[(((int64_t)img * g.Cin + c) * g.H + hi) * g.W + wi];
+  col[row * HWo + hw] = v;
+}
+
+// dX[c][h][w] = sum over (kh, kw) in order of dcol[k][ho*Wo + wo] for the
+// output positions whose window covers (h, w) (kernels.cu:50-87, gathered)
+template <typename T>
+__global__ void __launch_bounds__(256) col2im_t_kernel(const T* __restrict__ dcol, T* __restrict__ dX, ConvGeom g,
+                                                       int imgs) {
+  const int64_t per_img = (int64_t)g.Cin * g.H * g.W;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= per_img * imgs) return;
+  const int64_t img = idx / per_img, rem = idx % per_img;
+  const int w = static_cast<int>(rem % g.W);
+  const int h = static_cast<int>((rem / g.W) % g.H);
+  const int c = static_cast<int>(rem / ((int64_t)g.W * g.H));
+  const int HWo = g.Ho * g.Wo;
+  dcol += img * ((int64_t)g.Cin * g.Kh * g.Kw) * HWo;
+  float acc = 0.f;
+  for (int kh = 0; kh < g.Kh; ++kh) {
+    const int hn = h + g.ph - kh * g.dh;
+    if (hn < 0 || hn % g.sh) continue;
+    const int ho = hn / g.sh;
+    if (ho >= g.Ho) continue;
+    for (int kw = 0; kw < g.Kw; ++kw) {
+      const int wn = w + g.pw - kw * g.dw;
+      if (wn < 0 || wn % g.sw) continue;
+      const int wo = wn / g.sw;
+      if (wo >= g.Wo) continue;
+      const int k = (c * g.Kh + kh) * g.Kw + kw;
+      acc += Elem<T>::load1(dcol + (int64_t)k * HWo + ho * g.Wo + wo);
+    }
+  }
+  Elem<T>::store1(dX + idx, acc);
+}
+
+// acc[i] = (first ? 0 : acc[i]) + src[0*n + i] + src[1*n + i] + ... (slices in order)
+template <typename T>
+__global__ void __launch_bounds__(256) acc_add_kernel(float* __restrict__ acc, const T* __restrict__ src, int64_t n,
+                                                      int slices, int first) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v = first ? 0.f : acc[i];
+  for (int j = 0; j < slices; ++j) v += Elem<T>::load1(src + (int64_t)j * n + i);
+  acc[i] = v;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) acc_store_kernel(T* __restrict__ dst, const float* __restrict__ acc, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) Elem<T>::store1(dst + i, acc[i]);
+}
+
+template <typename T>
+static hipError_t launch_im2col(const void* X, void* col, const ConvGeom& g, int imgs, hipStream_t s) {
+  const int64_t rows = (int64_t)imgs * g.Cin * g.Kh * g.Kw;
+  const int hw_blocks = (g.Ho * g.Wo + 255) / 256;
+  if (rows * hw_blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((im2col_t_kernel<T>), dim3(static_cast<unsigned>(rows * hw_blocks)), dim3(256), 0, s,
+                     static_cast<const T*>(X), static_cast<T*>(col), g, hw_blocks);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_col2im(const void* dcol, void* dX, const ConvGeom& g, int imgs, hipStream_t s) {
+  const int64_t total = (int64_t)g.Cin * g.H * g.W * imgs;
+  if ((total + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((col2im_t_kernel<T>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const T*>(dcol), static_cast<T*>(dX), g, imgs);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_acc_add(float* acc, const void* src, int64_t n, int slices, bool first, hipStream_t s) {
+  hipLaunchKernelGGL((acc_add_kernel<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, acc,
+                     static_cast<const T*>(src), n, slices, first ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_acc_store(void* dst, const float* acc, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL((acc_store_kernel<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                     static_cast<T*>(dst), acc, n);
+  return hipGetLastError();
+}
+
+#define GEV2_DISPATCH_T(dtype, F, ...)                            \
+  ((dtype) == GEV2_F32 ? F<float>(__VA_ARGS__)                    \
+   : (dtype) == GEV2_BF16 ? F<__bf16>(__VA_ARGS__)                \
+                          : F<_Float16>(__VA_ARGS__))
+
+}  // namespace gev2
+
+namespace {
+
+thread_local std::string t_conv_error;
+
+int conv_fail(int st, const char* msg) {
+  t_conv_error = msg;
+  return st;
+}
+
+size_t esize(int dtype) { return dtype == GEV2_F32 ? 4 : 2; }
+
+// Shape validation shared by forward and backward (launcher.cu:110-144, 241-276).
+template <typename D>
+int conv_check(const D* d, gev2::ConvGeom* g) {
+  if (!d) return conv_fail(GEV2_INVALID_ARGUMENT, "null descriptor");
+  if (d->dtype != GEV2_F32 && d->dtype != GEV2_F16 && d->dtype != GEV2_BF16)
+    return conv_fail(GEV2_DTYPE_MISMATCH, "dtype must be F32, F16 or BF16");
+  if (d->act < GEV2_ACT_NONE || d->act > GEV2_ACT_TANH) return conv_fail(GEV2_INVALID_ARGUMENT, "bad act kind");
+  if (d->groups != 1) return conv_fail(GEV2_UNIMPLEMENTED, "groups != 1");
+  if (d->N <= 0 || d->Cin <= 0 || d->H <= 0 || d->W <= 0 || d->Cout <= 0 || d->Kh <= 0 || d->Kw <= 0 ||
+      d->stride_h <= 0 || d->stride_w <= 0 || d->dil_h <= 0 || d->dil_w <= 0 || d->pad_h < 0 || d->pad_w < 0)
+    return conv_fail(GEV2_INVALID, "non-positive dimension, stride or dilation, or negative padding");
+  g->Cin = d->Cin; g->H = d->H; g->W = d->W; g->Kh = d->Kh; g->Kw = d->Kw;
+  g->sh = d->stride_h; g->sw = d->stride_w; g->ph = d->pad_h; g->pw = d->pad_w; g->dh = d->dil_h; g->dw = d->dil_w;
+  g->Ho = (d->H + 2 * d->pad_h - d->dil_h * (d->Kh - 1) - 1) / d->stride_h + 1;
+  g->Wo = (d->W + 2 * d->pad_w - d->dil_w * (d->Kw - 1) - 1) / d->stride_w + 1;
+  if (g->Ho <= 0 || g->Wo <= 0) return conv_fail(GEV2_INVALID, "empty output");
+  const int64_t K = (int64_t)d->Cin * d->Kh * d->Kw, HWo = (int64_t)g->Ho * g->Wo;
+  if (K * HWo > 0x7fffffffLL || (int64_t)d->Cout * HWo > 0x7fffffffLL || (int64_t)d->Cin * d->H * d->W > 0x7fffffffLL)
+    return conv_fail(GEV2_INVALID, "per-image sizes must fit int32");
+  return GEV2_OK;
+}
+
+int gemm_status(int st) {
+  if (st != GEV2_OK) t_conv_error = std::string("gemm: ") + gev2_last_error();
+  return st;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return GEV2_OK;
+  t_conv_error = std::string(where) + ": " + hipGetErrorString(e);
+  return GEV2_HIP_ERROR;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gev2_conv2d_last_error(void) { return t_conv_error.c_str(); }
+
+int gev2_conv2d_fwd(const gev2_conv2d_desc* d, void* stream) {
+  t_conv_error.clear();
+  gev2::ConvGeom g{};
+  int st = conv_check(d, &g);
+  if (st != GEV2_OK) return st;
+  if (!d->X || !d->Wt) return conv_fail(GEV2_MISSING_INPUT, "X / W is null");
+  if (!d->Y) return conv_fail(GEV2_MISSING_OUTPUT, "Y is null");
+  if (d->save_z && !d->Z) return conv_fail(GEV2_MISSING_OUTPUT, "save_z requires Z");
+  const int64_t K = (int64_t)d->Cin * d->Kh * d->Kw, HWo = (int64_t)g.Ho * g.Wo;
+  const int64_t per_img = K * HWo * static_cast<int64_t>(esize(d->dtype));
+  if (!d->col || d->col_bytes < per_img) return conv_fail(GEV2_MISSING_INPUT, "col workspace smaller than one image");
+  const int chunk = static_cast<int>(std::min<int64_t>(d->N, d->col_bytes / per_img));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const size_t es = esize(d->dtype);
+  for (int n0 = 0; n0 < d->N; n0 += chunk) {
+    const int c = std::min(chunk, d->N - n0);
+    const char* x = static_cast<const char*>(d->X) + (size_t)n0 * d->Cin * d->H * d->W * es;
+    st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_im2col, x, d->col, g, c, s), "im2col");
+    if (st != GEV2_OK) return st;
+    gev2_gemm_fwd_desc f{};
+    f.dtype = d->dtype; f.act = d->act; f.leaky_slope = d->leaky_slope; f.alpha = 1.f;
+    f.bias_kind = d->bias ? GEV2_BIAS_PER_M : GEV2_BIAS_NONE;
+    f.M = d->Cout; f.N = HWo; f.K = K; f.batch = c;
+    f.A = d->Wt; f.lda = K; f.stride_a = 0;
+    f.B = d->col; f.ldb = HWo; f.stride_b = K * HWo;
+    f.bias = d->bias; f.stride_bias = 0;
+    f.Y = static_cast<char*>(d->Y) + (size_t)n0 * d->Cout * HWo * es; f.ldy = HWo; f.stride_y = d->Cout * HWo;
+    if (d->save_z) {
+      f.Z = static_cast<char*>(d->Z) + (size_t)n0 * d->Cout * HWo * es; f.ldz = HWo; f.stride_z = d->Cout * HWo;
+    }
+    st = gemm_status(gev2_gemm_fwd(&f, stream));
+    if (st != GEV2_OK) return st;
+  }
+  return GEV2_OK;
+}
+
+int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* d, void* stream) {
+  t_conv_error.clear();
+  gev2::ConvGeom g{};
+  int st = conv_check(d, &g);
+  if (st != GEV2_OK) return st;
+  if (!d->X || !d->Wt || !d->dY || !d->Z) return conv_fail(GEV2_MISSING_INPUT, "X / W / dY / Z is null");
+  if (!d->dW && !d->dB && !d->dX) return GEV2_OK;
+  const int64_t K = (int64_t)d->Cin * d->Kh * d->Kw, HWo = (int64_t)g.Ho * g.Wo, CK = (int64_t)d->Cout * K;
+  const int64_t es = static_cast<int64_t>(esize(d->dtype));
+  // images per batched call: what every workspace in use holds
+  int64_t chunk = d->N;
+  auto fit = [&chunk](int64_t bytes, int64_t per_img) { chunk = std::min(chunk, bytes / per_img); };
+  if (!d->col) return conv_fail(GEV2_MISSING_INPUT, "col workspace is required");
+  fit(d->col_bytes, K * HWo * es);
+  if (d->dX) {
+    if (!d->dcol) return conv_fail(GEV2_MISSING_INPUT, "dX needs the dcol workspace");
+    fit(d->dcol_bytes, K * HWo * es);
+  }
+  if (d->dW) {
+    if (!d->gw || !d->acc_w) return conv_fail(GEV2_MISSING_INPUT, "dW needs the gw and acc_w workspaces");
+    fit(d->gw_bytes, CK * es);
+  }
+  if (d->dB) {
+    if (!d->acc_b) return conv_fail(GEV2_MISSING_INPUT, "dB needs the acc_b workspace");
+    fit(d->acc_b_bytes - 4 * (int64_t)d->Cout, 4 * (int64_t)d->Cout);
+  }
+  if (chunk < 1) return conv_fail(GEV2_MISSING_INPUT, "a workspace is smaller than one image needs");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  float* accW = d->acc_w;               // [Cout*K] sum of dW_n
+  float* accB = d->acc_b;               // [Cout]   sum of dB_n
+  float* gb = d->acc_b + d->Cout;       // [chunk][Cout] dB_n
+  for (int64_t n0 = 0; n0 < d->N; n0 += chunk) {
+    const int c = static_cast<int>(std::min<int64_t>(chunk, d->N - n0));
+    const char* x = static_cast<const char*>(d->X) + n0 * d->Cin * d->H * d->W * es;
+    st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_im2col, x, d->col, g, c, s), "im2col");
+    if (st != GEV2_OK) return st;
+    gev2_gemm_bwd_desc b{};
+    b.dtype = d->dtype; b.act = d->act; b.leaky_slope = d->leaky_slope; b.alpha = 1.f; b.beta = 0.f;
+    b.bias_kind = d->dB ? GEV2_BIAS_PER_M : GEV2_BIAS_NONE;
+    b.M = d->Cout; b.N = HWo; b.K = K; b.batch = c;
+    b.A = d->Wt; b.lda = K; b.stride_a = 0;
+    b.B = d->col; b.ldb = HWo; b.stride_b = K * HWo;
+    b.gY = static_cast<const char*>(d->dY) + n0 * d->Cout * HWo * es; b.ldgy = HWo; b.stride_gy = d->Cout * HWo;
+    b.Z = static_cast<const char*>(d->Z) + n0 * d->Cout * HWo * es; b.ldz = HWo; b.stride_z = d->Cout * HWo;
+    if (d->dW) { b.gA = d->gw; b.ldga = K; b.stride_ga = CK; }
+    if (d->dX) { b.gB = d->dcol; b.ldgb = HWo; b.stride_gb = K * HWo; }
+    if (d->dB) { b.gBias = gb; b.stride_gbias = d->Cout; }
+    b.workspace = d->dz; b.workspace_bytes = d->dz_bytes;
+    st = gemm_status(gev2_gemm_bwd(&b, stream));
+    if (st != GEV2_OK) return st;
+    if (d->dW) {
+      st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_add, accW, d->gw, CK, c, n0 == 0, s), "acc dW");
+      if (st != GEV2_OK) return st;
+    }
+    if (d->dB) {
+      st = hip_status(gev2::launch_acc_add<float>(accB, gb, d->Cout, c, n0 == 0, s), "acc dB");
+      if (st != GEV2_OK) return st;
+    }
+    if (d->dX) {
+      char* dx = static_cast<char*>(d->dX) + n0 * d->Cin * d->H * d->W * es;
+      st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_col2im, d->dcol, dx, g, c, s), "col2im");
+      if (st != GEV2_OK) return st;
+    }
+  }
+  if (d->dW) {
+    st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_store, d->dW, accW, CK, s), "store dW");
+    if (st != GEV2_OK) return st;
+  }
+  if (d->dB) {
+    st = hip_status(hipMemcpyAsync(d->dB, accB, sizeof(float) * d->Cout, hipMemcpyDeviceToDevice, s), "store dB");
+    if (st != GEV2_OK) return st;
+  }
+  return GEV2_OK;
+}
+
+}  // extern "C"

@@ -27,6 +27,7 @@ EXPORTED = [
     "gev2_stream_destroy", "gev2_stream_synchronize", "gev2_device_synchronize",
     "gev2_event_create", "gev2_event_destroy", "gev2_event_record", "gev2_event_synchronize",
     "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16",
+    "gev2_conv2d_fwd", "gev2_conv2d_bwd", "gev2_conv2d_last_error",
 ]
 
 
@@ -59,6 +60,36 @@ class BwdDesc(ctypes.Structure):
         ("gC", ctypes.c_void_p), ("ldgc", ctypes.c_int64), ("stride_gc", ctypes.c_int64),
         ("gBias", ctypes.c_void_p), ("stride_gbias", ctypes.c_int64),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+_CONV_GEOM = [
+    ("N", ctypes.c_int32), ("Cin", ctypes.c_int32), ("H", ctypes.c_int32), ("W", ctypes.c_int32),
+    ("Cout", ctypes.c_int32), ("Kh", ctypes.c_int32), ("Kw", ctypes.c_int32),
+    ("stride_h", ctypes.c_int32), ("stride_w", ctypes.c_int32), ("pad_h", ctypes.c_int32),
+    ("pad_w", ctypes.c_int32), ("dil_h", ctypes.c_int32), ("dil_w", ctypes.c_int32), ("groups", ctypes.c_int32),
+]
+
+
+class Conv2dDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("act", ctypes.c_int32), ("leaky_slope", ctypes.c_float),
+        ("save_z", ctypes.c_int32), *_CONV_GEOM,
+        ("X", ctypes.c_void_p), ("Wt", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("Y", ctypes.c_void_p),
+        ("Z", ctypes.c_void_p), ("col", ctypes.c_void_p), ("col_bytes", ctypes.c_int64),
+    ]
+
+
+class Conv2dBwdDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("act", ctypes.c_int32), ("leaky_slope", ctypes.c_float),
+        ("reserved0", ctypes.c_int32), *_CONV_GEOM,
+        ("X", ctypes.c_void_p), ("Wt", ctypes.c_void_p), ("dY", ctypes.c_void_p), ("Z", ctypes.c_void_p),
+        ("dW", ctypes.c_void_p), ("dB", ctypes.c_void_p), ("dX", ctypes.c_void_p),
+        ("col", ctypes.c_void_p), ("col_bytes", ctypes.c_int64), ("dcol", ctypes.c_void_p),
+        ("dcol_bytes", ctypes.c_int64), ("gw", ctypes.c_void_p), ("gw_bytes", ctypes.c_int64),
+        ("acc_b", ctypes.c_void_p), ("acc_b_bytes", ctypes.c_int64), ("acc_w", ctypes.c_void_p),
+        ("dz", ctypes.c_void_p), ("dz_bytes", ctypes.c_int64),
     ]
 
 
@@ -113,6 +144,10 @@ def lib() -> ctypes.CDLL:
     L.gev2_event_synchronize.argtypes = [vp]
     L.gev2_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
     L.gev2_probe_mfma_bf16.argtypes = [i32, i32, vp]
+    L.gev2_conv2d_fwd.argtypes = [ctypes.POINTER(Conv2dDesc), vp]
+    L.gev2_conv2d_bwd.argtypes = [ctypes.POINTER(Conv2dBwdDesc), vp]
+    L.gev2_conv2d_last_error.restype = ctypes.c_char_p
+    L.gev2_conv2d_last_error.argtypes = []
     _lib = L
     return L
 
@@ -121,6 +156,13 @@ def check(status: int, where: str) -> None:
     if status != 0:
         L = lib()
         raise GemmError(status, where, (L.gev2_last_error() or b"").decode()
+                        or L.gev2_status_string(status).decode())
+
+
+def check_conv(status: int, where: str) -> None:
+    if status != 0:
+        L = lib()
+        raise GemmError(status, where, (L.gev2_conv2d_last_error() or b"").decode()
                         or L.gev2_status_string(status).decode())
 
 

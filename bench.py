@@ -22,6 +22,7 @@ totalling > 256 MB so that reads come from HBM, not the MALL.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -243,6 +244,52 @@ def conv_cfg(ctx, dtype, iters):
             "gbps": byt / (ms * 1e-3) / 1e9, "roofline_frac": t_roof / (ms * 1e-3)}
 
 
+def conv_op_cfg(ctx, dtype, iters, images_per_call):
+    """C5a through the conv2d operator (gev2_conv2d_fwd / _bwd): X[32,64,56,56], W[128,64,3,3],
+    3x3 / stride 1 / pad 1, bias + ReLU, Z saved; im2col + batched GEMM forward, and the backward
+    (dW, dB, dX) with workspaces for `images_per_call` images per batched call."""
+    capi = ctx.capi
+    N, Cin, H, Wd, Cout, Kh, Kw = 32, 64, 56, 56, 128, 3, 3
+    K, HWo = Cin * Kh * Kw, H * Wd
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(56)
+    X = capi.to_storage(g.random((N, Cin, H, Wd), dtype=np.float32), dtype)
+    W = capi.to_storage(normal(g, (Cout, Cin, Kh, Kw), np.sqrt(2 / K)), dtype)
+    dY = capi.to_storage(normal(g, (N, Cout, H, Wd)), dtype)
+    b = normal(g, (Cout,), 0.02)
+    pX, pW, pdY, pb = ctx.put(X), ctx.put(W), ctx.put(dY), ctx.put(b)
+    pY, pZ = ctx.empty(N * Cout * HWo * es), ctx.empty(N * Cout * HWo * es)
+    pdW, pdB, pdX = ctx.empty(Cout * K * es), ctx.empty(Cout * 4), ctx.empty(N * Cin * H * Wd * es)
+    c = images_per_call
+    col_bytes = c * K * HWo * es
+    pcol, pdcol, pgw = ctx.empty(col_bytes), ctx.empty(col_bytes), ctx.empty(c * Cout * K * es)
+    acc_b_bytes = (c + 1) * Cout * 4
+    pacc_w, pacc_b = ctx.empty(Cout * K * 4), ctx.empty(acc_b_bytes)
+    dz_bytes = ((c * Cout * HWo * es + 255) // 256) * 256
+    pdz = ctx.empty(dz_bytes)
+    geom = dict(N=N, Cin=Cin, H=H, W=Wd, Cout=Cout, Kh=Kh, Kw=Kw, stride_h=1, stride_w=1, pad_h=1, pad_w=1,
+                dil_h=1, dil_w=1, groups=1)
+    fd = capi.Conv2dDesc(dtype=dtype, act=capi.ACT["relu"], save_z=1, X=pX, Wt=pW, bias=pb, Y=pY, Z=pZ,
+                         col=pcol, col_bytes=col_bytes, **geom)
+    bd = capi.Conv2dBwdDesc(dtype=dtype, act=capi.ACT["relu"], X=pX, Wt=pW, dY=pdY, Z=pZ, dW=pdW, dB=pdB, dX=pdX,
+                            col=pcol, col_bytes=col_bytes, dcol=pdcol, dcol_bytes=col_bytes, gw=pgw,
+                            gw_bytes=c * Cout * K * es, acc_b=pacc_b, acc_b_bytes=acc_b_bytes, acc_w=pacc_w,
+                            dz=pdz, dz_bytes=dz_bytes, **geom)
+    L = capi.lib()
+
+    def fwd():
+        capi.check_conv(L.gev2_conv2d_fwd(ctypes.byref(fd), ctx.stream.ptr), "conv fwd")
+
+    def bwd():
+        capi.check_conv(L.gev2_conv2d_bwd(ctypes.byref(bd), ctx.stream.ptr), "conv bwd")
+
+    fwd_ms = ctx.time_ms(fwd, iters)
+    bwd_ms = ctx.time_ms(bwd, iters)
+    flop = 2.0 * N * HWo * K * Cout
+    return {"images_per_call": c, "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
+            "tflops_fwd": flop / (fwd_ms * 1e-3) / 1e12, "tflops_bwd": 2 * flop / (bwd_ms * 1e-3) / 1e12}
+
+
 def skinny_cfg(ctx, iters, sets=10):
     """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL.
     The split-K partials go to a caller workspace (gev2_gemm_fwd_workspace_size)."""
@@ -361,6 +408,9 @@ def main():
             ("c4_sdpa_bf16", lambda: sdpa_cfg(ctx, capi.BF16, 50)),
             ("c5a_conv_f32", lambda: conv_cfg(ctx, capi.F32, 20)),
             ("c5a_conv_bf16", lambda: conv_cfg(ctx, capi.BF16, 20)),
+            ("c5a_conv2d_op_f32_per_image", lambda: conv_op_cfg(ctx, capi.F32, 5, 1)),
+            ("c5a_conv2d_op_f32", lambda: conv_op_cfg(ctx, capi.F32, 5, 32)),
+            ("c5a_conv2d_op_bf16", lambda: conv_op_cfg(ctx, capi.BF16, 10, 32)),
             ("c5b_skinny_bf16", lambda: skinny_cfg(ctx, 100)),
         ]
         for key, fn in todo:

@@ -147,6 +147,75 @@ int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* desc);
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
 
 /*
+ * 2-D convolution, NCHW, groups = 1, on the operator (replaces
+ * Conv2DCudaLaunch / Conv2DCudaBackwardLaunch, conv2d/api.hpp:47-69,
+ * conv2d/launcher.cu:106-459):
+ *   Ho = (H + 2*pad_h - dil_h*(Kh-1) - 1) / stride_h + 1, likewise Wo;
+ *   Z[n,co,ho,wo] = sum_{c,kh,kw} W[co,c,kh,kw] * X[n,c,ho*stride_h-pad_h+kh*dil_h,
+ *                   wo*stride_w-pad_w+kw*dil_w] (zero outside) + bias[co];  Y = act(Z).
+ * X [N,Cin,H,W], W [Cout,Cin,Kh,Kw], bias [Cout] fp32 (optional), Y / Z
+ * [N,Cout,Ho,Wo], all contiguous.  K = Cin*Kh*Kw, HWo = Ho*Wo.
+ * col: im2col workspace of at least K*HWo elements (one image); a larger one
+ * lets one GEMM launch cover floor(col_bytes / (K*HWo*elem)) images.
+ */
+typedef struct gev2_conv2d_desc {
+  int32_t dtype;
+  int32_t act;
+  float leaky_slope;
+  int32_t save_z;                 /* 1: write Z (must be non-NULL) */
+  int32_t N, Cin, H, W, Cout, Kh, Kw;
+  int32_t stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, groups;
+  const void* X;
+  const void* Wt;
+  const float* bias;
+  void* Y;
+  void* Z;
+  void* col;  int64_t col_bytes;
+} gev2_conv2d_desc;
+
+/*
+ * Backward: dW [Cout,Cin,Kh,Kw], dB [Cout] fp32, dX [N,Cin,H,W] (each optional),
+ * from dY and the saved Z (both [N,Cout,Ho,Wo]); dW and dB are sums over all
+ * images.  Workspaces, per image of a chunk (elements of dtype unless noted):
+ *   col         K*HWo            im2col (always)
+ *   dcol        K*HWo            gradient columns (when dX)
+ *   gw          Cout*K           that image's dW (when dW)
+ *   acc_b       Cout floats      that image's dB, after Cout floats of the sum (when dB)
+ * and once:
+ *   acc_w       Cout*K floats    fp32 sum of dW over images (when dW)
+ *   dz          optional dY' scratch of the operator backward (see
+ *               gev2_gemm_bwd_desc.workspace), dz_bytes its size
+ * One batched operator backward covers as many images as every workspace in
+ * use holds (*_bytes); the results do not depend on that chunk size.
+ */
+typedef struct gev2_conv2d_bwd_desc {
+  int32_t dtype;
+  int32_t act;
+  float leaky_slope;
+  int32_t reserved0;
+  int32_t N, Cin, H, W, Cout, Kh, Kw;
+  int32_t stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, groups;
+  const void* X;
+  const void* Wt;
+  const void* dY;
+  const void* Z;
+  void* dW;
+  float* dB;
+  void* dX;
+  void* col;    int64_t col_bytes;
+  void* dcol;   int64_t dcol_bytes;
+  void* gw;     int64_t gw_bytes;
+  float* acc_b; int64_t acc_b_bytes;
+  float* acc_w;
+  void* dz;     int64_t dz_bytes;
+} gev2_conv2d_bwd_desc;
+
+int gev2_conv2d_fwd(const gev2_conv2d_desc* desc, void* stream);
+int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* desc, void* stream);
+/* Message for the last failing conv2d call on this thread ("" if none). */
+const char* gev2_conv2d_last_error(void);
+
+/*
  * Benchmark helpers (no counterpart in the reference): issue `reps` calls back
  * to back on `stream`, call i using descs[i % n_descs] (rotating buffer sets),
  * so that a timing of small problems measures the device, not the caller.

@@ -22,9 +22,13 @@ It restates, in float64 NumPy, the host math of the reference:
 * the reference's own NumPy test math -- ``tests/cuda_pyd_test/smoke_gemm_binding.py:84-123``
 * batched slices       -- ``backends/cuda/ops/sdpa/launcher.cu:166-170``
   (slice (b,h) starts at ((b*H+h)*rows*cols))
+* 2-D convolution      -- ``backends/cuda/ops/conv2d/launcher.cu:106-459`` and
+  ``kernels.cu:12-87`` (output size, zero padding, dilation; column order
+  (c*Kh + kh)*Kw + kw; bias per output channel; dB summed over all images),
+  written here as direct sums over the kernel window, not as im2col
 
 Parity pins (what keeps this restatement honest) live in ``tests/test_oracle.py``:
-exact-integer brute force for the GEMMs, central finite differences for every
+exact-integer brute force for the GEMMs and the convolution (pure-Python loops), central finite differences for every
 activation derivative and for the backward (a scalar loss), the erf form of GELU
 for the tanh approximation, and the C restatement in ``gemm_oracle.c`` (fp32,
 sequential-k ``fmaf`` -- the reference's own small-kernel order).
@@ -340,3 +344,65 @@ def gelu_erf(z) -> np.ndarray:
     z = np.asarray(z, dtype=np.float64)
     erf = np.vectorize(math.erf)
     return 0.5 * z * (1.0 + erf(z / math.sqrt(2.0)))
+
+
+# ---------------------------------------------------------------------------
+# 2-D convolution (conv2d/launcher.cu:106-459, kernels.cu:12-87), float64
+# ---------------------------------------------------------------------------
+def conv2d_out_size(H: int, W: int, Kh: int, Kw: int, stride=(1, 1), pad=(0, 0), dil=(1, 1)) -> Tuple[int, int]:
+    """launcher.cu:134-135."""
+    Ho = (H + 2 * pad[0] - dil[0] * (Kh - 1) - 1) // stride[0] + 1
+    Wo = (W + 2 * pad[1] - dil[1] * (Kw - 1) - 1) // stride[1] + 1
+    return Ho, Wo
+
+
+def _window(Xp, kh, kw, Ho, Wo, stride, dil):
+    """X padded [N,C,Hp,Wp] -> the input samples under kernel tap (kh, kw): [N,C,Ho,Wo]."""
+    h0, w0 = kh * dil[0], kw * dil[1]
+    return Xp[:, :, h0:h0 + stride[0] * (Ho - 1) + 1:stride[0], w0:w0 + stride[1] * (Wo - 1) + 1:stride[1]]
+
+
+def conv2d_forward(X, W, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), act="none",
+                   slope: float = 0.01) -> Tuple[np.ndarray, np.ndarray]:
+    """Z[n,co] = sum_{c,kh,kw} W[co,c,kh,kw] * Xpad[n,c,ho*s+kh*d, wo*s+kw*d] + bias[co];
+    Y = act(Z).  Returns (Y, Z), float64 [N,Cout,Ho,Wo]."""
+    X = np.asarray(X, np.float64)
+    W = np.asarray(W, np.float64)
+    N, C, H, Wd = X.shape
+    Cout, C2, Kh, Kw = W.shape
+    assert C == C2
+    Ho, Wo = conv2d_out_size(H, Wd, Kh, Kw, stride, pad, dil)
+    Xp = np.pad(X, ((0, 0), (0, 0), (pad[0], pad[0]), (pad[1], pad[1])))
+    Z = np.zeros((N, Cout, Ho, Wo))
+    for kh in range(Kh):
+        for kw in range(Kw):
+            win = _window(Xp, kh, kw, Ho, Wo, stride, dil)            # [N,C,Ho,Wo]
+            Z += np.einsum("nchw,oc->nohw", win, W[:, :, kh, kw])
+    if bias is not None:
+        Z = Z + np.asarray(bias, np.float64).reshape(1, Cout, 1, 1)
+    return act_forward(Z, act, slope), Z
+
+
+def conv2d_backward(X, W, dY, Z, stride=(1, 1), pad=(0, 0), dil=(1, 1), act="none",
+                    slope: float = 0.01) -> dict:
+    """dZ = dY * act'(Z); dB[co] = sum over n, ho, wo of dZ; dW[co,c,kh,kw] = sum of
+    dZ * the tap's input samples; dX = the transpose scatter of dZ through W (zero padding
+    dropped).  float64."""
+    X = np.asarray(X, np.float64)
+    W = np.asarray(W, np.float64)
+    N, C, H, Wd = X.shape
+    Cout, _, Kh, Kw = W.shape
+    Ho, Wo = conv2d_out_size(H, Wd, Kh, Kw, stride, pad, dil)
+    dZ = np.asarray(dY, np.float64) * act_deriv(Z, act, slope)
+    Xp = np.pad(X, ((0, 0), (0, 0), (pad[0], pad[0]), (pad[1], pad[1])))
+    dXp = np.zeros_like(Xp)
+    dW = np.zeros_like(W)
+    for kh in range(Kh):
+        for kw in range(Kw):
+            win = _window(Xp, kh, kw, Ho, Wo, stride, dil)
+            dW[:, :, kh, kw] = np.einsum("nohw,nchw->oc", dZ, win)
+            h0, w0 = kh * dil[0], kw * dil[1]
+            dXp[:, :, h0:h0 + stride[0] * (Ho - 1) + 1:stride[0], w0:w0 + stride[1] * (Wo - 1) + 1:stride[1]] += \
+                np.einsum("nohw,oc->nchw", dZ, W[:, :, kh, kw])
+    dX = dXp[:, :, pad[0]:pad[0] + H, pad[1]:pad[1] + Wd]
+    return {"dZ": dZ, "dW": dW, "dB": dZ.sum(axis=(0, 2, 3)), "dX": dX}

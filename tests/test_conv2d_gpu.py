@@ -1,0 +1,154 @@
+"""GPU parity of conv2d on the operator (the _ops_conv2d module with the reference's
+workspace contract, conv2d/launcher.cu:106-459) against the float64 direct-sum oracle:
+forward with bias, activation and Z over stride / padding / dilation variants, the
+multi-image launch (dCol_bytes), exact-integer inputs for bit-exact index handling, and
+the backward's dW, dB (summed over every image) and dX."""
+import numpy as np
+import pytest
+
+from oracle import gemm_oracle as O
+from gemm_helpers import BF16, F32, rounded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env(gpu):
+    from graph_executor_v2.ops import _ops_conv2d as conv
+    from graph_executor_v2.ops.device_array import DeviceArray
+    return conv, DeviceArray
+
+
+GEOMS = {
+    "c5a-like": dict(N=3, Cin=8, H=10, W=12, Cout=16, Kh=3, Kw=3, stride=(1, 1), pad=(1, 1), dil=(1, 1)),
+    "stride2": dict(N=2, Cin=5, H=11, W=9, Cout=12, Kh=3, Kw=2, stride=(2, 1), pad=(0, 2), dil=(1, 1)),
+    "dilated": dict(N=2, Cin=4, H=9, W=10, Cout=8, Kh=2, Kw=3, stride=(1, 2), pad=(1, 0), dil=(2, 1)),
+}
+
+
+def _attrs(conv, g, act, with_bias, save_z):
+    a = conv.Conv2DAttrs()
+    a.stride_h, a.stride_w = g["stride"]
+    a.pad_h, a.pad_w = g["pad"]
+    a.dil_h, a.dil_w = g["dil"]
+    a.act = {"none": conv.ActKind.__members__["None"], "relu": conv.ActKind.ReLU, "tanh": conv.ActKind.Tanh,
+             "leakyrelu": conv.ActKind.LeakyReLU}[act]
+    a.with_bias = with_bias
+    a.save_z = save_z
+    return a
+
+
+def _run(env, g, X, W, b, act, dtype=F32, all_images=False, dY=None, bwd_images=1):
+    conv, DA = env
+    dt = "float32" if dtype == F32 else "bfloat16"
+    cdt = conv.DType.F32 if dtype == F32 else conv.DType.BF16
+    N, Cout = g["N"], g["Cout"]
+    Ho, Wo = O.conv2d_out_size(g["H"], g["W"], g["Kh"], g["Kw"], g["stride"], g["pad"], g["dil"])
+    K, HWo = g["Cin"] * g["Kh"] * g["Kw"], Ho * Wo
+    dX_, dW_, db_ = DA.from_numpy(X, dt), DA.from_numpy(W, dt), DA.from_numpy(b, "float32")
+    Y, Z = DA.empty((N, Cout, Ho, Wo), dt), DA.empty((N, Cout, Ho, Wo), dt)
+    col = DA.empty((N if all_images else 1, K * HWo), dt)
+    wkc, ytmp, zrows = DA.empty((K * Cout,)), DA.empty((HWo * Cout,)), DA.empty((HWo * Cout,))
+    a = _attrs(conv, g, act, True, True)
+    conv.forward(dX_.ptr, list(X.shape), dW_.ptr, list(W.shape), Y.ptr, list(Y.shape), bias_ptr=db_.ptr,
+                 z_ptr=Z.ptr, attrs=a, dCol_ptr=col.ptr, W_KC_ptr=wkc.ptr, Y_tmp_ptr=ytmp.ptr, Z_rows_ptr=zrows.ptr,
+                 dtype=cdt, dCol_bytes=col.nbytes if all_images else 0)
+    out = {"Y": Y.get(), "Z": Z.get()}
+    if dY is not None:
+        gdY = DA.from_numpy(dY, dt)
+        gW, gb, gX = DA.empty(W.shape, dt), DA.empty((Cout,), "float32"), DA.empty(X.shape, dt)
+        # the reference's backward workspaces (conv2d_pybind.cpp:163-166), kept alive for the call
+        # (bwd_images > 1: larger dCol / dTmp / W_CK, so that one batched call covers that many images)
+        c = bwd_images
+        bufs = dict(dCol_ptr=DA.empty((c, K * HWo), dt), dTmp_ptr=DA.empty((c, max(Cout * K, HWo * K))),
+                    W_CK_ptr=DA.empty((c, Cout * K)), dWpack_ptr=DA.empty((Cout * K,)),
+                    dY_HT_ptr=DA.empty((HWo * Cout,)), gy_rows_ptr=DA.empty((Cout * HWo,)),
+                    Z_rows_ptr=DA.empty((Cout * HWo,)))
+        sizes = {} if c == 1 else dict(dCol_bytes=bufs["dCol_ptr"].nbytes, dTmp_bytes=bufs["dTmp_ptr"].nbytes,
+                                       W_CK_bytes=bufs["W_CK_ptr"].nbytes)
+        conv.backward(dX_.ptr, list(X.shape), dW_.ptr, list(W.shape), gdY.ptr, list(dY.shape), Z.ptr, list(dY.shape),
+                      dw_ptr=gW.ptr, db_ptr=gb.ptr, dx_ptr=gX.ptr, attrs=a, dtype=cdt,
+                      **{k: v.ptr for k, v in bufs.items()}, **sizes)
+        out.update(dW=gW.get(), dB=gb.get(), dX=gX.get())
+    return out
+
+
+def _inputs(g, seed, integers=False):
+    r = np.random.default_rng(seed)
+    shapeX = (g["N"], g["Cin"], g["H"], g["W"])
+    shapeW = (g["Cout"], g["Cin"], g["Kh"], g["Kw"])
+    if integers:
+        return (r.integers(-3, 4, shapeX).astype(np.float32), r.integers(-2, 3, shapeW).astype(np.float32),
+                r.integers(-4, 5, g["Cout"]).astype(np.float32))
+    K = g["Cin"] * g["Kh"] * g["Kw"]
+    return (r.uniform(0, 1, shapeX).astype(np.float32),
+            (r.standard_normal(shapeW) * np.sqrt(2 / K)).astype(np.float32),
+            (0.02 * r.standard_normal(g["Cout"])).astype(np.float32))
+
+
+@pytest.mark.parametrize("geom", list(GEOMS))
+@pytest.mark.parametrize("all_images", [False, True], ids=["per-image", "one-launch"])
+def test_conv2d_forward_f32(env, geom, all_images):
+    g = GEOMS[geom]
+    X, W, b = _inputs(g, 1)
+    out = _run(env, g, X, W, b, "relu", all_images=all_images)
+    Y64, Z64 = O.conv2d_forward(X, W, b, g["stride"], g["pad"], g["dil"], act="relu")
+    np.testing.assert_allclose(out["Z"], Z64, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(out["Y"], Y64, rtol=1e-4, atol=1e-5)
+    pos = out["Z"] > 0
+    assert np.array_equal(out["Y"][pos], out["Z"][pos]) and np.all(out["Y"][~pos] == 0)
+
+
+@pytest.mark.parametrize("geom", list(GEOMS))
+@pytest.mark.parametrize("bwd_images", [1, 2, 3])
+def test_conv2d_exact_integers(env, geom, bwd_images):
+    """Integer inputs make every sum exact: index, padding and stride handling bit-exact,
+    for one image per backward call, for chunks that divide N, and for a ragged last chunk."""
+    g = GEOMS[geom]
+    X, W, b = _inputs(g, 2, integers=True)
+    dY = np.random.default_rng(3).integers(-2, 3, (g["N"], g["Cout"]) + O.conv2d_out_size(
+        g["H"], g["W"], g["Kh"], g["Kw"], g["stride"], g["pad"], g["dil"])).astype(np.float32)
+    out = _run(env, g, X, W, b, "none", all_images=True, dY=dY, bwd_images=bwd_images)
+    Y64, Z64 = O.conv2d_forward(X, W, b, g["stride"], g["pad"], g["dil"])
+    assert np.array_equal(out["Z"], Z64) and np.array_equal(out["Y"], Y64)
+    ref = O.conv2d_backward(X, W, dY, Z64, g["stride"], g["pad"], g["dil"])
+    for k in ("dX", "dW", "dB"):                    # dB: summed over every image
+        d = np.abs(out[k] - ref[k])
+        assert np.array_equal(out[k], ref[k]), (k, int((d > 0).sum()), float(d.max()),
+                                                np.unravel_index(int(np.argmax(d)), d.shape))
+
+
+@pytest.mark.parametrize("act", ["relu", "tanh", "leakyrelu"])
+@pytest.mark.parametrize("bwd_images", [1, 3])
+def test_conv2d_backward_f32(env, act, bwd_images):
+    g = GEOMS["c5a-like"]
+    X, W, b = _inputs(g, 4)
+    Ho, Wo = O.conv2d_out_size(g["H"], g["W"], g["Kh"], g["Kw"], g["stride"], g["pad"], g["dil"])
+    dY = np.random.default_rng(5).standard_normal((g["N"], g["Cout"], Ho, Wo)).astype(np.float32)
+    out = _run(env, g, X, W, b, act, dY=dY, bwd_images=bwd_images)
+    ref = O.conv2d_backward(X, W, dY, out["Z"].astype(np.float64), g["stride"], g["pad"], g["dil"], act=act)
+    np.testing.assert_allclose(out["dX"], ref["dX"], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(out["dW"], ref["dW"], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(out["dB"], ref["dB"], rtol=1e-4, atol=1e-4)
+
+
+def test_conv2d_bf16(env):
+    """bf16 tensors (additive): forward within one bf16 rounding of the fp32-accumulated
+    sum; gradients within 4*K*eps of their magnitude sums."""
+    g = GEOMS["c5a-like"]
+    X, W, b = _inputs(g, 6)
+    X, W = rounded(X, BF16).astype(np.float32), rounded(W, BF16).astype(np.float32)
+    Ho, Wo = O.conv2d_out_size(g["H"], g["W"], g["Kh"], g["Kw"], g["stride"], g["pad"], g["dil"])
+    dY = rounded(np.random.default_rng(7).standard_normal((g["N"], g["Cout"], Ho, Wo)), BF16).astype(np.float32)
+    out = _run(env, g, X, W, b, "relu", dtype=BF16, dY=dY, bwd_images=3)
+    Y64, Z64 = O.conv2d_forward(X, W, b, g["stride"], g["pad"], g["dil"], act="relu")
+    absZ, _ = O.conv2d_forward(np.abs(X), np.abs(W), np.abs(b), g["stride"], g["pad"], g["dil"])
+    K = g["Cin"] * g["Kh"] * g["Kw"]
+    assert np.all(np.abs(out["Z"] - Z64) <= 2.0 ** -8 * np.abs(Z64) + 1.01 * K * 2.0 ** -24 * absZ + 1e-7)
+    ref = O.conv2d_backward(X, W, dY, out["Z"].astype(np.float64), g["stride"], g["pad"], g["dil"], act="relu")
+    aref = O.conv2d_backward(np.abs(X), np.abs(W), np.abs(dY), np.ones_like(Z64), g["stride"], g["pad"], g["dil"])
+    eps = 2.0 ** -7
+    n_dx, n_dw = g["Cout"] * g["Kh"] * g["Kw"], g["N"] * Ho * Wo
+    assert np.all(np.abs(out["dX"] - ref["dX"]) <= 4 * n_dx * eps * aref["dX"] + 1e-6)
+    assert np.all(np.abs(out["dW"] - ref["dW"]) <= 4 * n_dw * eps * aref["dW"] + 1e-6)
+    assert np.all(np.abs(out["dB"] - ref["dB"]) <= 1e-3 * aref["dB"] + 1e-5)

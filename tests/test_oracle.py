@@ -312,3 +312,74 @@ def test_numpy_baseline_matches_oracle():
     r = O.gemm_backward(X, W, gY, Z, "relu", bias_kind=O.BIAS_PERN)
     assert np.allclose(Y, Y64, atol=1e-5) and np.allclose(gA, r["gA"], atol=1e-4)
     assert np.allclose(gB, r["gB"], atol=1e-4) and np.allclose(gb[0], r["gBias"], atol=1e-4)
+
+
+# ---------------------------------------------------------------------------
+# 2-D convolution
+# ---------------------------------------------------------------------------
+def _conv_brute(X, W, b, stride, pad, dil):
+    """Pure-Python integer loops over every output and tap (conv2d/kernels.cu:12-45 semantics)."""
+    N, C, H, Wd = X.shape
+    Co, _, Kh, Kw = W.shape
+    Ho, Wo = O.conv2d_out_size(H, Wd, Kh, Kw, stride, pad, dil)
+    out = [[[[0] * Wo for _ in range(Ho)] for _ in range(Co)] for _ in range(N)]
+    for n in range(N):
+        for co in range(Co):
+            for ho in range(Ho):
+                for wo in range(Wo):
+                    acc = int(b[co]) if b is not None else 0
+                    for c in range(C):
+                        for kh in range(Kh):
+                            for kw in range(Kw):
+                                hi = ho * stride[0] - pad[0] + kh * dil[0]
+                                wi = wo * stride[1] - pad[1] + kw * dil[1]
+                                if 0 <= hi < H and 0 <= wi < Wd:
+                                    acc += int(W[co, c, kh, kw]) * int(X[n, c, hi, wi])
+                    out[n][co][ho][wo] = acc
+    return np.array(out, dtype=np.float64)
+
+
+@pytest.mark.parametrize("geom", [((1, 1), (1, 1), (1, 1)), ((2, 1), (0, 2), (1, 1)), ((1, 2), (1, 0), (2, 1))],
+                         ids=["s1p1", "s2-pad0x2", "dil2"])
+def test_conv2d_forward_exact_integers(geom):
+    stride, pad, dil = geom
+    g = np.random.default_rng(31)
+    X = g.integers(-3, 4, (2, 3, 7, 6)).astype(np.float64)
+    W = g.integers(-2, 3, (4, 3, 3, 2)).astype(np.float64)
+    b = g.integers(-5, 6, 4).astype(np.float64)
+    Y, Z = O.conv2d_forward(X, W, b, stride, pad, dil, act="relu")
+    ref = _conv_brute(X, W, b, stride, pad, dil)
+    assert np.array_equal(Z, ref)
+    assert np.array_equal(Y, np.maximum(ref, 0))
+    assert O.conv2d_out_size(7, 6, 3, 2, stride, pad, dil) == Z.shape[2:]
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "tanh"])
+def test_conv2d_backward_matches_finite_difference(act):
+    """d/dX, d/dW, d/db of L = sum(dY * act(conv(X, W) + b)) by central differences."""
+    g = np.random.default_rng(33)
+    stride, pad, dil = (2, 1), (1, 1), (1, 2)
+    X = g.standard_normal((2, 2, 6, 7))
+    W = g.standard_normal((3, 2, 2, 3))
+    b = g.standard_normal(3)
+    _, Z = O.conv2d_forward(X, W, b, stride, pad, dil, act=act)
+    dY = g.standard_normal(Z.shape)
+    grads = O.conv2d_backward(X, W, dY, Z, stride, pad, dil, act=act)
+
+    def loss(X_, W_, b_):
+        Y_, _ = O.conv2d_forward(X_, W_, b_, stride, pad, dil, act=act)
+        return float((dY * Y_).sum())
+
+    h = 1e-6
+    for name, arr, idxs in (("dX", X, [(0, 1, 2, 3), (1, 0, 5, 6), (0, 0, 0, 0)]),
+                            ("dW", W, [(2, 1, 1, 2), (0, 0, 0, 0)]), ("dB", b, [(1,)])):
+        for idx in idxs:
+            p, m = arr.copy(), arr.copy()
+            p[idx] += h
+            m[idx] -= h
+            args_p = [X, W, b]
+            args_m = [X, W, b]
+            k = {"dX": 0, "dW": 1, "dB": 2}[name]
+            args_p[k], args_m[k] = p, m
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * h)
+            assert abs(fd - grads[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (name, idx, fd, grads[name][idx])
