@@ -34,56 +34,173 @@ struct ConvGeom {
   int Cin, H, W, Kh, Kw, sh, sw, ph, pw, dh, dw, Ho, Wo;
 };
 
-// col[(img*K + k) * HWo + hw] = X[img][c][h_out*sh - ph + kh*dh][w_out*sw - pw + kw*dw] (0 outside);
-// one block per (row, 256 output positions), consecutive threads on consecutive hw
-template <typename T>
-__global__ void __launch_bounds__(256) im2col_t_kernel(const T* __restrict__ X, T* __restrict__ col, ConvGeom g,
-                                                       int hw_blocks) {
-  const int HWo = g.Ho * g.Wo;
-  const int K = g.Cin * g.Kh * g.Kw;
-  const int64_t row = blockIdx.x / hw_blocks;       // img*K + k
-  const int hw = static_cast<int>(blockIdx.x % hw_blocks) * 256 + threadIdx.x;
-  if (hw >= HWo) return;
-  const int img = static_cast<int>(row / K), k = static_cast<int>(row % K);
-  const int kw = k % g.Kw, kh = (k / g.Kw) % g.Kh, c = k / (g.Kw * g.Kh);
-  const int ho = hw / g.Wo, wo = hw % g.Wo;
-  const int hi = ho * g.sh - g.ph + kh * g.dh, wi = wo * g.sw - g.pw + kw * g.dw;
-  T v{};
-  if (static_cast<unsigned>(hi) < static_cast<unsigned>(g.H) && static_cast<unsigned>(wi) < static_cast<unsigned>(g.W))
-    v = X[(((int64_t)img * g.Cin + c) * g.H + hi) * g.W + wi];
-  col[row * HWo + hw] = v;
+// Raw storage word of T: im2col and col2im's scatter-free gather move bits.
+template <typename T> struct Word { using type = uint16_t; };
+template <> struct Word<float> { using type = uint32_t; };
+
+constexpr int kRun = 8;   // consecutive outputs per thread (one 16-byte store of a 16-bit type)
+
+// Store a thread's run of kRun words at dst: as 16-byte pieces when `vec`
+// (the run is whole and 16-byte aligned), else element by element up to n.
+template <typename U>
+__device__ __forceinline__ void store_run(U* dst, const U (&v)[kRun], int n, bool vec) {
+  if (vec && n >= kRun) {
+    constexpr int kWords = 16 / sizeof(U);
+#pragma unroll
+    for (int q = 0; q < kRun / kWords; ++q) {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(U) == 2) w[i] = static_cast<uint32_t>(v[q * kWords + 2 * i]) |
+                                             (static_cast<uint32_t>(v[q * kWords + 2 * i + 1]) << 16);
+        else w[i] = v[q * kWords + i];
+      }
+      *reinterpret_cast<u32x4*>(dst + q * kWords) = w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRun; ++j)
+      if (j < n) dst[j] = v[j];
+  }
 }
 
-// dX[c][h][w] = sum over (kh, kw) in order of dcol[k][ho*Wo + wo] for the
-// output positions whose window covers (h, w) (kernels.cu:50-87, gathered)
+// col[(img*K + k) * HWo + hw] = X[img][c][ho*sh - ph + kh*dh][wo*sw - pw + kw*dw] (0 outside),
+// k = (c*Kh + kh)*Kw + kw, hw = ho*Wo + wo (kernels.cu:12-45).  A thread writes
+// kRun consecutive hw of one (img, k) row; its row and window offsets are
+// derived once, then ho / wo advance incrementally.
 template <typename T>
-__global__ void __launch_bounds__(256) col2im_t_kernel(const T* __restrict__ dcol, T* __restrict__ dX, ConvGeom g,
-                                                       int imgs) {
-  const int64_t per_img = (int64_t)g.Cin * g.H * g.W;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= per_img * imgs) return;
-  const int64_t img = idx / per_img, rem = idx % per_img;
-  const int w = static_cast<int>(rem % g.W);
-  const int h = static_cast<int>((rem / g.W) % g.H);
-  const int c = static_cast<int>(rem / ((int64_t)g.W * g.H));
+__global__ void __launch_bounds__(256) im2col_t_kernel(const T* __restrict__ Xt, T* __restrict__ colt, ConvGeom g,
+                                                       int runs_per_row, int64_t threads, int vec) {
+  using U = typename Word<T>::type;
+  const U* __restrict__ X = reinterpret_cast<const U*>(Xt);
+  U* __restrict__ col = reinterpret_cast<U*>(colt);
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= threads) return;
   const int HWo = g.Ho * g.Wo;
-  dcol += img * ((int64_t)g.Cin * g.Kh * g.Kw) * HWo;
-  float acc = 0.f;
-  for (int kh = 0; kh < g.Kh; ++kh) {
-    const int hn = h + g.ph - kh * g.dh;
-    if (hn < 0 || hn % g.sh) continue;
-    const int ho = hn / g.sh;
-    if (ho >= g.Ho) continue;
-    for (int kw = 0; kw < g.Kw; ++kw) {
-      const int wn = w + g.pw - kw * g.dw;
-      if (wn < 0 || wn % g.sw) continue;
-      const int wo = wn / g.sw;
-      if (wo >= g.Wo) continue;
-      const int k = (c * g.Kh + kh) * g.Kw + kw;
-      acc += Elem<T>::load1(dcol + (int64_t)k * HWo + ho * g.Wo + wo);
+  const int K = g.Cin * g.Kh * g.Kw;
+  const int64_t row = t / runs_per_row;             // img*K + k
+  const int hw0 = static_cast<int>(t - row * runs_per_row) * kRun;
+  const int img = static_cast<int>(row / K), k = static_cast<int>(row - (int64_t)img * K);
+  const int kw = k % g.Kw, kh = (k / g.Kw) % g.Kh, c = k / (g.Kw * g.Kh);
+  int ho = hw0 / g.Wo, wo = hw0 - ho * g.Wo;
+  const U* __restrict__ xp = X + ((int64_t)img * g.Cin + c) * g.H * g.W;
+  const int hoff = kh * g.dh - g.ph, woff = kw * g.dw - g.pw;
+  U v[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    const int hi = ho * g.sh + hoff, wi = wo * g.sw + woff;
+    const bool in = hw0 + j < HWo && static_cast<unsigned>(hi) < static_cast<unsigned>(g.H) &&
+                    static_cast<unsigned>(wi) < static_cast<unsigned>(g.W);
+    v[j] = in ? xp[hi * g.W + wi] : U(0);
+    if (++wo == g.Wo) { wo = 0; ++ho; }
+  }
+  store_run(col + row * HWo + hw0, v, HWo - hw0, vec != 0);
+}
+
+// The same col through LDS: a workgroup owns one (img, c) input plane and a
+// band of TH output rows.  It reads the R = (TH-1)*sh + (Kh-1)*dh + 1 input
+// rows the band needs into LDS once (rows outside the image as zeros), then
+// writes the Kh*Kw col rows of the band as runs of kRun consecutive hw, so X
+// is read from HBM once instead of Kh*Kw times through the caches.
+template <typename T>
+__global__ void __launch_bounds__(256) im2col_lds_kernel(const T* __restrict__ Xt, T* __restrict__ colt, ConvGeom g,
+                                                         int TH, int bands, int vec, int xvec) {
+  using U = typename Word<T>::type;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  U* lds = reinterpret_cast<U*>(lds_raw);
+  const int band = static_cast<int>(blockIdx.x % bands);
+  const int64_t ic = blockIdx.x / bands;            // img*Cin + c
+  const int img = static_cast<int>(ic / g.Cin), c = static_cast<int>(ic - (int64_t)img * g.Cin);
+  const int ho0 = band * TH;
+  const int rows = min(TH, g.Ho - ho0);
+  const int R = (rows - 1) * g.sh + (g.Kh - 1) * g.dh + 1;
+  const int hbase = ho0 * g.sh - g.ph;
+  const U* __restrict__ xp = reinterpret_cast<const U*>(Xt) + ic * g.H * g.W;
+  if (xvec) {
+    // rows are whole 16-byte chunks (and the plane starts on one): copy chunks
+    constexpr int kWords = 16 / sizeof(U);
+    const int cpr = g.W / kWords, chunks = R * cpr;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < chunks; i += 256) {
+      const int r = i / cpr;
+      const int hi = hbase + r;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (static_cast<unsigned>(hi) < static_cast<unsigned>(g.H))
+        v = *reinterpret_cast<const u32x4*>(xp + (int64_t)hi * g.W + (i - r * cpr) * kWords);
+      *reinterpret_cast<u32x4*>(lds + i * kWords) = v;
+    }
+  } else {
+#pragma unroll 8
+    for (int i = threadIdx.x; i < R * g.W; i += 256) {
+      const int r = i / g.W;
+      const int hi = hbase + r;
+      lds[i] = static_cast<unsigned>(hi) < static_cast<unsigned>(g.H) ? xp[hi * g.W + (i - r * g.W)] : U(0);
     }
   }
-  Elem<T>::store1(dX + idx, acc);
+  __syncthreads();
+  const int KK = g.Kh * g.Kw, HWo = g.Ho * g.Wo, K = g.Cin * KK;
+  const int n_out = rows * g.Wo;
+  const int runs = (n_out + kRun - 1) / kRun;
+  U* __restrict__ col = reinterpret_cast<U*>(colt) + ((int64_t)img * K + (int64_t)c * KK) * HWo + ho0 * g.Wo;
+  for (int run = threadIdx.x; run < KK * runs; run += 256) {
+    const int kidx = run / runs;
+    const int o0 = (run - kidx * runs) * kRun;
+    const int kh = kidx / g.Kw, kw = kidx - kh * g.Kw;
+    int hl = o0 / g.Wo, wo = o0 - hl * g.Wo;
+    const int woff = kw * g.dw - g.pw;
+    U v[kRun];
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const int wi = wo * g.sw + woff;
+      const bool in = o0 + j < n_out && static_cast<unsigned>(wi) < static_cast<unsigned>(g.W);
+      v[j] = in ? lds[(hl * g.sh + kh * g.dh) * g.W + wi] : U(0);
+      if (++wo == g.Wo) { wo = 0; ++hl; }
+    }
+    store_run(col + (int64_t)kidx * HWo + o0, v, n_out - o0, vec != 0);
+  }
+}
+
+// dX[img][c][h][w] = sum over (kh, kw), in that order, of dcol[k][ho*Wo + wo]
+// for the output positions whose window covers (h, w) (kernels.cu:50-87, as a
+// gather: no atomics, a fixed summation order).  A thread computes kRun
+// consecutive w of one (img, c, h) row; the kh terms are shared by the run.
+template <typename T>
+__global__ void __launch_bounds__(256) col2im_t_kernel(const T* __restrict__ dcol, T* __restrict__ dXt, ConvGeom g,
+                                                       int runs_per_row, int64_t threads, int vec) {
+  using U = typename Word<T>::type;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= threads) return;
+  const int64_t row = t / runs_per_row;             // (img*Cin + c)*H + h
+  const int w0 = static_cast<int>(t - row * runs_per_row) * kRun;
+  const int h = static_cast<int>(row % g.H);
+  const int64_t ic = row / g.H;                     // img*Cin + c
+  const int img = static_cast<int>(ic / g.Cin), c = static_cast<int>(ic - (int64_t)img * g.Cin);
+  const int HWo = g.Ho * g.Wo;
+  const int K = g.Cin * g.Kh * g.Kw;
+  const T* __restrict__ base = dcol + ((int64_t)img * K + (int64_t)c * g.Kh * g.Kw) * HWo;
+  float acc[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) acc[j] = 0.f;
+  for (int kh = 0; kh < g.Kh; ++kh) {
+    const int hn = h + g.ph - kh * g.dh;
+    if (hn < 0) break;                              // hn only falls as kh grows
+    const int ho = hn / g.sh;
+    if (ho * g.sh != hn || ho >= g.Ho) continue;
+    const T* __restrict__ rowp = base + (int64_t)kh * g.Kw * HWo + ho * g.Wo;
+    for (int kw = 0; kw < g.Kw; ++kw) {
+      const T* __restrict__ p = rowp + (int64_t)kw * HWo;
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        const int wn = w0 + j + g.pw - kw * g.dw;
+        const int wo = wn / g.sw;
+        if (w0 + j < g.W && wn >= 0 && wo * g.sw == wn && wo < g.Wo) acc[j] += Elem<T>::load1(p + wo);
+      }
+    }
+  }
+  U v[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) v[j] = static_cast<U>(Elem<T>::bits(acc[j]));
+  store_run(reinterpret_cast<U*>(dXt) + row * g.W + w0, v, g.W - w0, vec != 0);
 }
 
 // acc[i] = (first ? 0 : acc[i]) + src[0*n + i] + src[1*n + i] + ... (slices in order)
@@ -103,22 +220,46 @@ __global__ void __launch_bounds__(256) acc_store_kernel(T* __restrict__ dst, con
   if (i < n) Elem<T>::store1(dst + i, acc[i]);
 }
 
+constexpr int kIm2colLdsBytes = 32 * 1024;
+
 template <typename T>
 static hipError_t launch_im2col(const void* X, void* col, const ConvGeom& g, int imgs, hipStream_t s) {
-  const int64_t rows = (int64_t)imgs * g.Cin * g.Kh * g.Kw;
-  const int hw_blocks = (g.Ho * g.Wo + 255) / 256;
-  if (rows * hw_blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((im2col_t_kernel<T>), dim3(static_cast<unsigned>(rows * hw_blocks)), dim3(256), 0, s,
-                     static_cast<const T*>(X), static_cast<T*>(col), g, hw_blocks);
+  const int64_t HWo = (int64_t)g.Ho * g.Wo;
+  // LDS band: the most output rows whose input rows fit in kIm2colLdsBytes
+  int TH = g.Ho;
+  auto band_bytes = [&g](int th) { return ((int64_t)(th - 1) * g.sh + (int64_t)(g.Kh - 1) * g.dh + 1) * g.W * sizeof(T); };
+  while (TH > 1 && band_bytes(TH) > kIm2colLdsBytes) TH = (TH + 1) / 2;
+  if (band_bytes(TH) <= kIm2colLdsBytes) {
+    const int bands = (g.Ho + TH - 1) / TH;
+    const int64_t blocks = (int64_t)imgs * g.Cin * bands;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    // 16-byte stores: every band starts on a 16-byte boundary of its col row
+    const int vec = (HWo * (int64_t)sizeof(T)) % 16 == 0 && ((int64_t)TH * g.Wo * sizeof(T)) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(col) % 16 == 0;
+    const int xvec = ((int64_t)g.W * sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0;
+    hipLaunchKernelGGL((im2col_lds_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                       static_cast<unsigned>(band_bytes(TH)), s, static_cast<const T*>(X), static_cast<T*>(col), g,
+                       TH, bands, vec, xvec);
+    return hipGetLastError();
+  }
+  const int runs = static_cast<int>((HWo + kRun - 1) / kRun);
+  const int64_t threads = (int64_t)imgs * g.Cin * g.Kh * g.Kw * runs;
+  if ((threads + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+  // 16-byte stores: every row starts on a 16-byte boundary
+  const int vec = (HWo * (int64_t)sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(col) % 16 == 0;
+  hipLaunchKernelGGL((im2col_t_kernel<T>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const T*>(X), static_cast<T*>(col), g, runs, threads, vec);
   return hipGetLastError();
 }
 
 template <typename T>
 static hipError_t launch_col2im(const void* dcol, void* dX, const ConvGeom& g, int imgs, hipStream_t s) {
-  const int64_t total = (int64_t)g.Cin * g.H * g.W * imgs;
-  if ((total + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((col2im_t_kernel<T>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const T*>(dcol), static_cast<T*>(dX), g, imgs);
+  const int runs = (g.W + kRun - 1) / kRun;
+  const int64_t threads = (int64_t)imgs * g.Cin * g.H * runs;
+  if ((threads + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+  const int vec = ((int64_t)g.W * sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(dX) % 16 == 0;
+  hipLaunchKernelGGL((col2im_t_kernel<T>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const T*>(dcol), static_cast<T*>(dX), g, runs, threads, vec);
   return hipGetLastError();
 }
 

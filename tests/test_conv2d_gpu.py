@@ -99,6 +99,18 @@ def test_conv2d_forward_f32(env, geom, all_images):
     assert np.array_equal(out["Y"][pos], out["Z"][pos]) and np.all(out["Y"][~pos] == 0)
 
 
+@pytest.mark.parametrize("width", [1000, 999], ids=["aligned", "odd"])
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_conv2d_wide_planes(env, width, dtype):
+    """Planes too wide for one LDS band of im2col (the band is split into row groups), with
+    16-byte-aligned rows and with an odd width (element stores); exact-integer inputs, bit-exact."""
+    g = dict(N=2, Cin=2, H=40, W=width, Cout=4, Kh=3, Kw=3, stride=(1, 1), pad=(1, 1), dil=(1, 1))
+    X, W, b = _inputs(g, 8, integers=True)
+    out = _run(env, g, X, W, b, "none", dtype=dtype, all_images=True)
+    Y64, Z64 = O.conv2d_forward(X, W, b, g["stride"], g["pad"], g["dil"])
+    assert np.array_equal(out["Z"], Z64) and np.array_equal(out["Y"], Y64)
+
+
 @pytest.mark.parametrize("geom", list(GEOMS))
 @pytest.mark.parametrize("bwd_images", [1, 2, 3])
 def test_conv2d_exact_integers(env, geom, bwd_images):

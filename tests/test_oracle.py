@@ -383,3 +383,50 @@ def test_conv2d_backward_matches_finite_difference(act):
             args_p[k], args_m[k] = p, m
             fd = (loss(*args_p) - loss(*args_m)) / (2 * h)
             assert abs(fd - grads[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (name, idx, fd, grads[name][idx])
+
+
+def test_conv2d_1x1_is_the_plain_gemm():
+    """A 1x1 / stride 1 / pad 0 convolution is, per image, W[Cout,Cin] . X_n[Cin, H*W] + b."""
+    g = np.random.default_rng(35)
+    X = g.standard_normal((2, 5, 4, 3))
+    W = g.standard_normal((6, 5, 1, 1))
+    b = g.standard_normal(6)
+    _, Z = O.conv2d_forward(X, W, b)
+    for n in range(2):
+        _, ref = O.gemm_forward(W[:, :, 0, 0], X[n].reshape(5, 12), b, O.BIAS_PERM)
+        assert np.allclose(Z[n].reshape(6, 12), ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("geom", [((1, 1), (1, 1), (1, 1)), ((2, 1), (0, 2), (1, 1)), ((1, 2), (1, 0), (2, 1))],
+                         ids=["s1p1", "s2-pad0x2", "dil2"])
+def test_conv2d_backward_exact_integers(geom):
+    """dX / dW / dB against pure-Python integer loops over every output and tap (act none)."""
+    stride, pad, dil = geom
+    g = np.random.default_rng(37)
+    X = g.integers(-3, 4, (2, 3, 7, 6)).astype(np.float64)
+    W = g.integers(-2, 3, (4, 3, 3, 2)).astype(np.float64)
+    N, C, H, Wd = X.shape
+    Co, _, Kh, Kw = W.shape
+    Ho, Wo = O.conv2d_out_size(H, Wd, Kh, Kw, stride, pad, dil)
+    dY = g.integers(-3, 4, (N, Co, Ho, Wo)).astype(np.float64)
+    r = O.conv2d_backward(X, W, dY, np.zeros_like(dY), stride, pad, dil)
+    dX = [[[[0] * Wd for _ in range(H)] for _ in range(C)] for _ in range(N)]
+    dW = [[[[0] * Kw for _ in range(Kh)] for _ in range(C)] for _ in range(Co)]
+    dB = [0] * Co
+    for n in range(N):
+        for co in range(Co):
+            for ho in range(Ho):
+                for wo in range(Wo):
+                    d = int(dY[n, co, ho, wo])
+                    dB[co] += d
+                    for c in range(C):
+                        for kh in range(Kh):
+                            for kw in range(Kw):
+                                hi = ho * stride[0] - pad[0] + kh * dil[0]
+                                wi = wo * stride[1] - pad[1] + kw * dil[1]
+                                if 0 <= hi < H and 0 <= wi < Wd:
+                                    dW[co][c][kh][kw] += d * int(X[n, c, hi, wi])
+                                    dX[n][c][hi][wi] += d * int(W[co, c, kh, kw])
+    assert np.array_equal(r["dX"], np.array(dX, dtype=np.float64))
+    assert np.array_equal(r["dW"], np.array(dW, dtype=np.float64))
+    assert np.array_equal(r["dB"], np.array(dB, dtype=np.float64))
