@@ -6,6 +6,7 @@ Outputs (next to the Python package, like the reference's CMake output dir
   graph_executor_v2/ops/_ops_common*.so   pybind11: shared shim types
   graph_executor_v2/ops/_ops_gemm*.so     pybind11: the GEMM op surface
   graph_executor_v2/ops/_ops_conv2d*.so   pybind11: conv2d on the GEMM op
+  graph_executor_v2/ops/_ops_rnn*.so      pybind11: Elman RNN on the GEMM op
 
 Usage: python ai_framework-dev_amd/build.py [--force] [-j N]
 """
@@ -29,7 +30,7 @@ INCLUDE = os.path.join(REPO, "include")
 HIP_SOURCES = [
     "gemm_tile_f32.hip", "gemm_tile_bf16.hip", "gemm_tile_f16.hip",
     "gemm_dl_bf16.hip", "gemm_dl_f16.hip",
-    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "probe.hip",
+    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "rnn.hip", "probe.hip",
 ]
 HIP_HEADERS = ["gev2_device.hpp", "gev2_kernels.hpp", "gemm_tile_impl.hpp", "gemm_dl_impl.hpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -44,8 +45,9 @@ BIND_SOURCES = {
     "_ops_common": ["bindings/ops_common_pybind.cpp"],
     "_ops_gemm": ["bindings/gemm_pybind.cpp", "host/gemm_host.cpp"],
     "_ops_conv2d": ["bindings/conv2d_pybind.cpp", "host/conv2d_host.cpp"],
+    "_ops_rnn": ["bindings/rnn_pybind.cpp", "host/rnn_host.cpp"],
 }
-HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp"]
+HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp", "host/rnn_host.hpp"]
 
 
 def _newer(target: str, deps: list[str]) -> bool:
@@ -104,7 +106,7 @@ def build_bindings(force: bool, jobs: int) -> list[str]:
                    "-fvisibility=hidden",
                    f"-I{pybind11.get_include()}", f"-I{py_inc}", f"-I{INCLUDE}", f"-I{CSRC}",
                    *paths, "-o", out + ".tmp"]
-            if mod in ("_ops_gemm", "_ops_conv2d"):
+            if mod in ("_ops_gemm", "_ops_conv2d", "_ops_rnn"):
                 cmd += [f"-L{OUT_DIR}", "-lgev2", "-Wl,-rpath,$ORIGIN"]
             cmds.append((cmd, out))
 

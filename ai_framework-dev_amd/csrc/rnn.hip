@@ -1,0 +1,310 @@
+// Elman RNN on the GEMM operator: the rnn launcher of graph_executor_v2
+// (backends/cuda/ops/rnn/launcher.cu:129-383, kernels.cu) rebuilt around it.
+//
+//   h_t = act(X_t Wx + h_{t-1} Wh + b),  Y[:,t,:] = h_t,  Z[:,t,:] = pre-activation,
+//   X [N,T,I], Wx [I,H], Wh [H,H], h0 [N,H], b [H] fp32, Y / Z [N,T,H].
+//
+// Forward, per step: one gather kernel writes XH = [X_t, h_{t-1}] ([N, I+H]),
+// then ONE operator forward XH . [Wx; Wh] (+ b, act) writes h_t and Z_t
+// straight into Y[:,t,:] and Z[:,t,:] through their row stride T*H, and the
+// next step reads h_t from Y.  The reference copies X_t and h_{t-1} in with
+// two 2-D copies and Y_rows / Z_rows out with two more per step.
+// Backward (BPTT), per step from T-1 down to 0: one gather kernel rebuilds
+// XH = [X_t, act(Z_{t-1}) or h0], forms G = dY_t + dh_next (dh_next = the
+// h-columns of the previous step's dXH) and stores the previous step's dX;
+// then ONE operator backward with gY = G, Z = Z[:,t,:] (stride T*H) gives
+// dXH = G' [Wx; Wh]^T, dWcat_t = XH^T G' and dB_t; one kernel adds dWcat_t
+// and dB_t to fp32 sums in step order.  dB is the sum over all steps (the
+// reference's per-step GEMM backward zero-fills it, so it keeps step 0's only).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "../../include/gev2_gemm.h"
+#include "gev2_device.hpp"
+
+namespace gev2 {
+
+struct RnnDims {
+  int N, T, I, H;
+};
+
+// xh[n, :I] = X[n, t, :];  xh[n, I:] = hprev[n * ldh + :]
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_fwd_gather_kernel(const T* __restrict__ X, const T* __restrict__ hprev,
+                                                             int64_t ldh, T* __restrict__ xh, RnnDims d, int t) {
+  const int IH = d.I + d.H;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)d.N * IH) return;
+  const int n = static_cast<int>(idx / IH), j = static_cast<int>(idx - (int64_t)n * IH);
+  xh[idx] = j < d.I ? X[((int64_t)n * d.T + t) * d.I + j] : hprev[n * ldh + (j - d.I)];
+}
+
+// Step t of the backward (T > t >= 0):
+//   xh[n, :I]  = X[n, t, :]
+//   xh[n, I:]  = t > 0 ? act(Z[n, t-1, :]) : h0[n, :]
+//   g[n, :]    = dY[n, t, :] + (t < T-1 ? dxh[n, I:] : 0)
+//   dX[n, t+1, :] = dxh[n, :I]            (t < T-1, dX requested)
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_bwd_gather_kernel(const T* __restrict__ X, const T* __restrict__ Z,
+                                                             const T* __restrict__ h0, const T* __restrict__ dY,
+                                                             const T* __restrict__ dxh, T* __restrict__ xh,
+                                                             T* __restrict__ g, T* __restrict__ dX, RnnDims d, int t,
+                                                             int act, float slope) {
+  const int IH = d.I + d.H;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)d.N * IH) return;
+  const int n = static_cast<int>(idx / IH), j = static_cast<int>(idx - (int64_t)n * IH);
+  const bool last = t == d.T - 1;
+  if (j < d.I) {
+    xh[idx] = X[((int64_t)n * d.T + t) * d.I + j];
+    if (dX && !last) dX[((int64_t)n * d.T + t + 1) * d.I + j] = dxh[idx];
+  } else {
+    const int h = j - d.I;
+    if (t > 0)
+      Elem<T>::store1(xh + idx, act_fwd(Elem<T>::load1(Z + ((int64_t)n * d.T + t - 1) * d.H + h), act, slope));
+    else
+      xh[idx] = h0[(int64_t)n * d.H + h];
+    float gy = Elem<T>::load1(dY + ((int64_t)n * d.T + t) * d.H + h);
+    if (!last) gy += Elem<T>::load1(dxh + idx);
+    Elem<T>::store1(g + (int64_t)n * d.H + h, gy);
+  }
+}
+
+// dwcat[i] = (first ? 0 : dwcat[i]) + tmpw[i];  dB[h] likewise from gb
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_acc_kernel(float* __restrict__ dwcat, const T* __restrict__ tmpw,
+                                                      int64_t nw, float* __restrict__ dB, const float* __restrict__ gb,
+                                                      int H, int first) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < nw) {
+    const float v = Elem<T>::load1(tmpw + i);
+    dwcat[i] = first ? v : dwcat[i] + v;
+  }
+  if (dB && i < H) dB[i] = first ? gb[i] : dB[i] + gb[i];
+}
+
+// After step 0: dX[n, 0, :] = dxh[n, :I]; dh0 = dxh[n, I:]; dWx / dWh = dwcat
+// split and converted to the tensor dtype.
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_bwd_finish_kernel(const T* __restrict__ dxh, const float* __restrict__ dwcat,
+                                                             T* __restrict__ dX, T* __restrict__ dh0,
+                                                             T* __restrict__ dWx, T* __restrict__ dWh, RnnDims d) {
+  const int IH = d.I + d.H;
+  const int64_t nx = (int64_t)d.N * IH, nw = (int64_t)IH * d.H;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < nx) {
+    const int n = static_cast<int>(idx / IH), j = static_cast<int>(idx - (int64_t)n * IH);
+    if (j < d.I) {
+      if (dX) dX[(int64_t)n * d.T * d.I + j] = dxh[idx];
+    } else if (dh0) {
+      dh0[(int64_t)n * d.H + (j - d.I)] = dxh[idx];
+    }
+  } else if (idx < nx + nw) {
+    const int64_t w = idx - nx;
+    const int64_t split = (int64_t)d.I * d.H;
+    if (w < split) {
+      if (dWx) Elem<T>::store1(dWx + w, dwcat[w]);
+    } else if (dWh) {
+      Elem<T>::store1(dWh + (w - split), dwcat[w]);
+    }
+  }
+}
+
+// T == 0: the gradients are zero (the reference zero-fills them first).
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_zero_kernel(T* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = T{};
+}
+
+inline unsigned blocks_for(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
+
+template <typename T>
+hipError_t launch_fwd_gather(const void* X, const void* hprev, int64_t ldh, void* xh, const RnnDims& d, int t,
+                             hipStream_t s) {
+  hipLaunchKernelGGL((rnn_fwd_gather_kernel<T>), dim3(blocks_for((int64_t)d.N * (d.I + d.H))), dim3(256), 0, s,
+                     static_cast<const T*>(X), static_cast<const T*>(hprev), ldh, static_cast<T*>(xh), d, t);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_bwd_gather(const void* X, const void* Z, const void* h0, const void* dY, const void* dxh, void* xh,
+                             void* g, void* dX, const RnnDims& d, int t, int act, float slope, hipStream_t s) {
+  hipLaunchKernelGGL((rnn_bwd_gather_kernel<T>), dim3(blocks_for((int64_t)d.N * (d.I + d.H))), dim3(256), 0, s,
+                     static_cast<const T*>(X), static_cast<const T*>(Z), static_cast<const T*>(h0),
+                     static_cast<const T*>(dY), static_cast<const T*>(dxh), static_cast<T*>(xh), static_cast<T*>(g),
+                     static_cast<T*>(dX), d, t, act, slope);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_acc(float* dwcat, const void* tmpw, int64_t nw, float* dB, const float* gb, int H, bool first,
+                      hipStream_t s) {
+  hipLaunchKernelGGL((rnn_acc_kernel<T>), dim3(blocks_for(std::max<int64_t>(nw, H))), dim3(256), 0, s, dwcat,
+                     static_cast<const T*>(tmpw), nw, dB, gb, H, first ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_bwd_finish(const void* dxh, const float* dwcat, void* dX, void* dh0, void* dWx, void* dWh,
+                             const RnnDims& d, hipStream_t s) {
+  const int64_t n = (int64_t)d.N * (d.I + d.H) + (int64_t)(d.I + d.H) * d.H;
+  hipLaunchKernelGGL((rnn_bwd_finish_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, s, static_cast<const T*>(dxh),
+                     dwcat, static_cast<T*>(dX), static_cast<T*>(dh0), static_cast<T*>(dWx), static_cast<T*>(dWh), d);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_zero(void* p, int64_t n, hipStream_t s) {
+  if (!p || n == 0) return hipSuccess;
+  hipLaunchKernelGGL((rnn_zero_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, s, static_cast<T*>(p), n);
+  return hipGetLastError();
+}
+
+#define GEV2_RNN_DISPATCH(dtype, F, ...)                          \
+  ((dtype) == GEV2_F32 ? F<float>(__VA_ARGS__)                    \
+   : (dtype) == GEV2_BF16 ? F<__bf16>(__VA_ARGS__)                \
+                          : F<_Float16>(__VA_ARGS__))
+
+}  // namespace gev2
+
+namespace {
+
+thread_local std::string t_rnn_error;
+
+int rnn_fail(int st, const char* msg) {
+  t_rnn_error = msg;
+  return st;
+}
+
+int64_t esize(int dtype) { return dtype == GEV2_F32 ? 4 : 2; }
+
+template <typename D>
+int rnn_check(const D* d) {
+  if (!d) return rnn_fail(GEV2_INVALID_ARGUMENT, "null descriptor");
+  if (d->dtype != GEV2_F32 && d->dtype != GEV2_F16 && d->dtype != GEV2_BF16)
+    return rnn_fail(GEV2_DTYPE_MISMATCH, "dtype must be F32, F16 or BF16");
+  if (d->act < GEV2_ACT_NONE || d->act > GEV2_ACT_TANH) return rnn_fail(GEV2_INVALID_ARGUMENT, "bad act kind");
+  if (d->N <= 0 || d->T < 0 || d->I <= 0 || d->H <= 0)
+    return rnn_fail(GEV2_INVALID, "N, I, H must be positive and T non-negative");
+  if ((int64_t)d->N * d->T * std::max(d->I, d->H) > 0x7fffffffLL ||
+      (int64_t)d->N * (d->I + d->H) > 0x7fffffffLL || (int64_t)(d->I + d->H) * d->H > 0x7fffffffLL)
+    return rnn_fail(GEV2_INVALID, "sizes must fit int32");
+  return GEV2_OK;
+}
+
+int gemm_status(int st) {
+  if (st != GEV2_OK) t_rnn_error = std::string("gemm: ") + gev2_last_error();
+  return st;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return GEV2_OK;
+  t_rnn_error = std::string(where) + ": " + hipGetErrorString(e);
+  return GEV2_HIP_ERROR;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gev2_rnn_last_error(void) { return t_rnn_error.c_str(); }
+
+int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
+  t_rnn_error.clear();
+  int st = rnn_check(d);
+  if (st != GEV2_OK) return st;
+  if (!d->X || !d->Wx || !d->Wh || !d->h0) return rnn_fail(GEV2_MISSING_INPUT, "X / Wx / Wh / h0 is null");
+  if (!d->Y) return rnn_fail(GEV2_MISSING_OUTPUT, "Y is null");
+  if (d->save_z && !d->Z) return rnn_fail(GEV2_MISSING_OUTPUT, "save_z requires Z");
+  if (d->save_z && d->Z == d->Y) return rnn_fail(GEV2_INVALID, "Z must not alias Y");
+  if (!d->xh || !d->wcat) return rnn_fail(GEV2_MISSING_INPUT, "xh and wcat workspaces are required");
+  const gev2::RnnDims dm{d->N, d->T, d->I, d->H};
+  const int64_t es = esize(d->dtype), IH = d->I + d->H;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // wcat = [Wx ; Wh]  ([I+H, H])
+  st = hip_status(hipMemcpyAsync(d->wcat, d->Wx, (size_t)d->I * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wx");
+  if (st != GEV2_OK) return st;
+  st = hip_status(hipMemcpyAsync(static_cast<char*>(d->wcat) + (size_t)d->I * d->H * es, d->Wh,
+                                 (size_t)d->H * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wh");
+  if (st != GEV2_OK) return st;
+  const int64_t ldy = (int64_t)d->T * d->H;
+  for (int t = 0; t < d->T; ++t) {
+    const void* hprev = t == 0 ? d->h0 : static_cast<const char*>(d->Y) + (size_t)(t - 1) * d->H * es;
+    st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_fwd_gather, d->X, hprev, t == 0 ? d->H : ldy, d->xh,
+                                      dm, t, s), "gather");
+    if (st != GEV2_OK) return st;
+    gev2_gemm_fwd_desc f{};
+    f.dtype = d->dtype; f.act = d->act; f.leaky_slope = d->leaky_slope; f.alpha = 1.f;
+    f.bias_kind = d->bias ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+    f.M = d->N; f.N = d->H; f.K = IH; f.batch = 1;
+    f.A = d->xh; f.lda = IH;
+    f.B = d->wcat; f.ldb = d->H;
+    f.bias = d->bias;
+    f.Y = static_cast<char*>(d->Y) + (size_t)t * d->H * es; f.ldy = ldy;
+    if (d->save_z) { f.Z = static_cast<char*>(d->Z) + (size_t)t * d->H * es; f.ldz = ldy; }
+    f.workspace = d->ws; f.workspace_bytes = d->ws_bytes;
+    st = gemm_status(gev2_gemm_fwd(&f, stream));
+    if (st != GEV2_OK) return st;
+  }
+  return GEV2_OK;
+}
+
+int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
+  t_rnn_error.clear();
+  int st = rnn_check(d);
+  if (st != GEV2_OK) return st;
+  if (!d->X || !d->Wx || !d->Wh || !d->h0 || !d->dY || !d->Z)
+    return rnn_fail(GEV2_MISSING_INPUT, "X / Wx / Wh / h0 / dY / Z is null");
+  if (!d->xh || !d->g || !d->wcat || !d->dxh || !d->dwcat || !d->tmpw || !d->gb)
+    return rnn_fail(GEV2_MISSING_INPUT, "workspaces xh, g, wcat, dxh, dwcat, tmpw and gb are required");
+  const gev2::RnnDims dm{d->N, d->T, d->I, d->H};
+  const int64_t es = esize(d->dtype), IH = d->I + d->H;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (d->T == 0) {
+    // no steps: every gradient is zero
+    st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_zero, d->dWx, (int64_t)d->I * d->H, s), "zero");
+    if (st == GEV2_OK) st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_zero, d->dWh, (int64_t)d->H * d->H, s), "zero");
+    if (st == GEV2_OK) st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_zero, d->dh0, (int64_t)d->N * d->H, s), "zero");
+    if (st == GEV2_OK) st = hip_status(gev2::launch_zero<float>(d->dB, d->H, s), "zero");
+    return st;
+  }
+  st = hip_status(hipMemcpyAsync(d->wcat, d->Wx, (size_t)d->I * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wx");
+  if (st != GEV2_OK) return st;
+  st = hip_status(hipMemcpyAsync(static_cast<char*>(d->wcat) + (size_t)d->I * d->H * es, d->Wh,
+                                 (size_t)d->H * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wh");
+  if (st != GEV2_OK) return st;
+  const int64_t ldz = (int64_t)d->T * d->H;
+  const bool want_w = d->dWx || d->dWh;
+  for (int t = d->T - 1; t >= 0; --t) {
+    st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_gather, d->X, d->Z, d->h0, d->dY, d->dxh, d->xh,
+                                      d->g, d->dX, dm, t, d->act, d->leaky_slope, s), "gather");
+    if (st != GEV2_OK) return st;
+    gev2_gemm_bwd_desc b{};
+    b.dtype = d->dtype; b.act = d->act; b.leaky_slope = d->leaky_slope; b.alpha = 1.f; b.beta = 0.f;
+    b.bias_kind = d->dB ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+    b.M = d->N; b.N = d->H; b.K = IH; b.batch = 1;
+    b.A = d->xh; b.lda = IH;
+    b.B = d->wcat; b.ldb = d->H;
+    b.gY = d->g; b.ldgy = d->H;
+    b.Z = static_cast<const char*>(d->Z) + (size_t)t * d->H * es; b.ldz = ldz;
+    b.gA = d->dxh; b.ldga = IH;
+    if (want_w) { b.gB = d->tmpw; b.ldgb = d->H; }
+    b.gBias = d->dB ? d->gb : nullptr;
+    b.workspace = d->ws; b.workspace_bytes = d->ws_bytes;
+    st = gemm_status(gev2_gemm_bwd(&b, stream));
+    if (st != GEV2_OK) return st;
+    if (want_w || d->dB) {
+      st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_acc, d->dwcat, d->tmpw, want_w ? IH * d->H : 0, d->dB,
+                                        d->gb, d->H, t == d->T - 1, s), "accumulate");
+      if (st != GEV2_OK) return st;
+    }
+  }
+  st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_finish, d->dxh, d->dwcat, d->dX, d->dh0, d->dWx,
+                                    d->dWh, dm, s), "finish");
+  return st;
+}
+
+}  // extern "C"

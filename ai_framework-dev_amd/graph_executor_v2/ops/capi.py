@@ -28,6 +28,7 @@ EXPORTED = [
     "gev2_event_create", "gev2_event_destroy", "gev2_event_record", "gev2_event_synchronize",
     "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16",
     "gev2_conv2d_fwd", "gev2_conv2d_bwd", "gev2_conv2d_last_error",
+    "gev2_rnn_fwd", "gev2_rnn_bwd", "gev2_rnn_last_error",
 ]
 
 
@@ -93,6 +94,30 @@ class Conv2dBwdDesc(ctypes.Structure):
     ]
 
 
+_RNN_HEAD = [("dtype", ctypes.c_int32), ("act", ctypes.c_int32), ("leaky_slope", ctypes.c_float)]
+_RNN_DIMS = [("N", ctypes.c_int32), ("T", ctypes.c_int32), ("I", ctypes.c_int32), ("H", ctypes.c_int32)]
+
+
+class RnnDesc(ctypes.Structure):
+    _fields_ = [
+        *_RNN_HEAD, ("save_z", ctypes.c_int32), *_RNN_DIMS,
+        ("X", ctypes.c_void_p), ("Wx", ctypes.c_void_p), ("Wh", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p), ("Y", ctypes.c_void_p), ("Z", ctypes.c_void_p), ("xh", ctypes.c_void_p),
+        ("wcat", ctypes.c_void_p), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_int64),
+    ]
+
+
+class RnnBwdDesc(ctypes.Structure):
+    _fields_ = [
+        *_RNN_HEAD, ("reserved0", ctypes.c_int32), *_RNN_DIMS,
+        ("X", ctypes.c_void_p), ("Wx", ctypes.c_void_p), ("Wh", ctypes.c_void_p), ("h0", ctypes.c_void_p),
+        ("dY", ctypes.c_void_p), ("Z", ctypes.c_void_p), ("dWx", ctypes.c_void_p), ("dWh", ctypes.c_void_p),
+        ("dB", ctypes.c_void_p), ("dh0", ctypes.c_void_p), ("dX", ctypes.c_void_p), ("xh", ctypes.c_void_p),
+        ("g", ctypes.c_void_p), ("wcat", ctypes.c_void_p), ("dxh", ctypes.c_void_p), ("dwcat", ctypes.c_void_p),
+        ("tmpw", ctypes.c_void_p), ("gb", ctypes.c_void_p), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_int64),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -148,6 +173,10 @@ def lib() -> ctypes.CDLL:
     L.gev2_conv2d_bwd.argtypes = [ctypes.POINTER(Conv2dBwdDesc), vp]
     L.gev2_conv2d_last_error.restype = ctypes.c_char_p
     L.gev2_conv2d_last_error.argtypes = []
+    L.gev2_rnn_fwd.argtypes = [ctypes.POINTER(RnnDesc), vp]
+    L.gev2_rnn_bwd.argtypes = [ctypes.POINTER(RnnBwdDesc), vp]
+    L.gev2_rnn_last_error.restype = ctypes.c_char_p
+    L.gev2_rnn_last_error.argtypes = []
     _lib = L
     return L
 
@@ -163,6 +192,13 @@ def check_conv(status: int, where: str) -> None:
     if status != 0:
         L = lib()
         raise GemmError(status, where, (L.gev2_conv2d_last_error() or b"").decode()
+                        or L.gev2_status_string(status).decode())
+
+
+def check_rnn(status: int, where: str) -> None:
+    if status != 0:
+        L = lib()
+        raise GemmError(status, where, (L.gev2_rnn_last_error() or b"").decode()
                         or L.gev2_status_string(status).decode())
 
 

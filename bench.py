@@ -290,6 +290,46 @@ def conv_op_cfg(ctx, dtype, iters, images_per_call):
             "tflops_fwd": flop / (fwd_ms * 1e-3) / 1e12, "tflops_bwd": 2 * flop / (bwd_ms * 1e-3) / 1e12}
 
 
+def rnn_op_cfg(ctx, dtype, iters, N=8, T=32, I=512, H=1024):
+    """Elman RNN through the operator (gev2_rnn_fwd / _bwd): X[N,T,I], tanh, bias, Z saved;
+    forward (T steps of gather + one operator GEMM [N, I+H] x [I+H, H]) and the backward through
+    time (dWx, dWh, dB, dh0, dX)."""
+    capi = ctx.capi
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(57)
+    X = capi.to_storage(normal(g, (N, T, I)), dtype)
+    Wx = capi.to_storage(normal(g, (I, H), 1 / np.sqrt(I)), dtype)
+    Wh = capi.to_storage(normal(g, (H, H), 0.5 / np.sqrt(H)), dtype)
+    h0 = capi.to_storage(normal(g, (N, H)), dtype)
+    dY = capi.to_storage(normal(g, (N, T, H)), dtype)
+    b = normal(g, (H,), 0.1)
+    pX, pWx, pWh, ph0, pdY, pb = (ctx.put(a) for a in (X, Wx, Wh, h0, dY, b))
+    pY, pZ = ctx.empty(N * T * H * es), ctx.empty(N * T * H * es)
+    IH = I + H
+    pxh, pwcat = ctx.empty(N * IH * es), ctx.empty(IH * H * es)
+    ws_bytes = 8 << 20
+    pws = ctx.empty(ws_bytes)
+    fd = capi.RnnDesc(dtype=dtype, act=capi.ACT["tanh"], save_z=1, N=N, T=T, I=I, H=H, X=pX, Wx=pWx, Wh=pWh,
+                      bias=pb, h0=ph0, Y=pY, Z=pZ, xh=pxh, wcat=pwcat, ws=pws, ws_bytes=ws_bytes)
+    bd = capi.RnnBwdDesc(dtype=dtype, act=capi.ACT["tanh"], N=N, T=T, I=I, H=H, X=pX, Wx=pWx, Wh=pWh, h0=ph0,
+                         dY=pdY, Z=pZ, dWx=ctx.empty(I * H * es), dWh=ctx.empty(H * H * es), dB=ctx.empty(H * 4),
+                         dh0=ctx.empty(N * H * es), dX=ctx.empty(N * T * I * es), xh=pxh, g=ctx.empty(N * H * es),
+                         wcat=pwcat, dxh=ctx.empty(N * IH * es), dwcat=ctx.empty(IH * H * 4),
+                         tmpw=ctx.empty(IH * H * es), gb=ctx.empty(H * 4), ws=pws, ws_bytes=ws_bytes)
+    L = capi.lib()
+
+    def fwd():
+        capi.check_rnn(L.gev2_rnn_fwd(ctypes.byref(fd), ctx.stream.ptr), "rnn fwd")
+
+    def bwd():
+        capi.check_rnn(L.gev2_rnn_bwd(ctypes.byref(bd), ctx.stream.ptr), "rnn bwd")
+
+    fwd_ms = ctx.time_ms(fwd, iters)
+    bwd_ms = ctx.time_ms(bwd, iters)
+    return {"shape": f"N={N} T={T} I={I} H={H} tanh", "fwd_us": fwd_ms * 1e3, "bwd_us": bwd_ms * 1e3,
+            "fwd_us_per_step": fwd_ms * 1e3 / T, "bwd_us_per_step": bwd_ms * 1e3 / T}
+
+
 def skinny_cfg(ctx, iters, sets=10):
     """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL.
     The split-K partials go to a caller workspace (gev2_gemm_fwd_workspace_size)."""
@@ -412,6 +452,8 @@ def main():
             ("c5a_conv2d_op_f32", lambda: conv_op_cfg(ctx, capi.F32, 5, 32)),
             ("c5a_conv2d_op_bf16", lambda: conv_op_cfg(ctx, capi.BF16, 10, 32)),
             ("c5b_skinny_bf16", lambda: skinny_cfg(ctx, 100)),
+            ("rnn_op_f32", lambda: rnn_op_cfg(ctx, capi.F32, 10)),
+            ("rnn_op_bf16", lambda: rnn_op_cfg(ctx, capi.BF16, 10)),
         ]
         for key, fn in todo:
             if only and key not in only:

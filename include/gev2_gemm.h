@@ -216,6 +216,73 @@ int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* desc, void* stream);
 const char* gev2_conv2d_last_error(void);
 
 /*
+ * Elman RNN on the operator (replaces RnnCudaLaunch / RnnCudaBackwardLaunch,
+ * rnn/api.hpp:55-79, rnn/launcher.cu:129-383):
+ *   h_t = act(X_t Wx + h_{t-1} Wh + b),  Y[:,t,:] = h_t,  Z[:,t,:] = pre-activation.
+ * X [N,T,I], Wx [I,H], Wh [H,H], h0 [N,H], bias [H] fp32 (optional), Y / Z
+ * [N,T,H], all contiguous, one dtype (F32 / F16 / BF16) except bias.
+ * Workspaces (elements of dtype): xh N*(I+H), wcat (I+H)*H.  ws / ws_bytes:
+ * optional scratch for the operator forward (gev2_gemm_fwd_desc.workspace).
+ * One gather kernel and one operator forward per step.
+ */
+typedef struct gev2_rnn_desc {
+  int32_t dtype;
+  int32_t act;
+  float leaky_slope;
+  int32_t save_z;                 /* 1: write Z (must be non-NULL, not Y) */
+  int32_t N, T, I, H;
+  const void* X;
+  const void* Wx;
+  const void* Wh;
+  const float* bias;
+  const void* h0;
+  void* Y;
+  void* Z;
+  void* xh;
+  void* wcat;
+  void* ws;  int64_t ws_bytes;
+} gev2_rnn_desc;
+
+/*
+ * Backward through time from dY (= dL/dY, [N,T,H]) and the saved Z: dWx,
+ * dWh, dB (fp32, sum over steps), dh0 and dX, each optional.  Workspaces
+ * (elements of dtype unless noted): xh N*(I+H), g N*H, wcat (I+H)*H,
+ * dxh N*(I+H), tmpw (I+H)*H, dwcat (I+H)*H floats, gb H floats.  ws / ws_bytes:
+ * optional dY' scratch of the operator backward (gev2_gemm_bwd_desc.workspace).
+ */
+typedef struct gev2_rnn_bwd_desc {
+  int32_t dtype;
+  int32_t act;
+  float leaky_slope;
+  int32_t reserved0;
+  int32_t N, T, I, H;
+  const void* X;
+  const void* Wx;
+  const void* Wh;
+  const void* h0;
+  const void* dY;
+  const void* Z;
+  void* dWx;
+  void* dWh;
+  float* dB;
+  void* dh0;
+  void* dX;
+  void* xh;
+  void* g;
+  void* wcat;
+  void* dxh;
+  float* dwcat;
+  void* tmpw;
+  float* gb;
+  void* ws;  int64_t ws_bytes;
+} gev2_rnn_bwd_desc;
+
+int gev2_rnn_fwd(const gev2_rnn_desc* desc, void* stream);
+int gev2_rnn_bwd(const gev2_rnn_bwd_desc* desc, void* stream);
+/* Message for the last failing RNN call on this thread ("" if none). */
+const char* gev2_rnn_last_error(void);
+
+/*
  * Benchmark helpers (no counterpart in the reference): issue `reps` calls back
  * to back on `stream`, call i using descs[i % n_descs] (rotating buffer sets),
  * so that a timing of small problems measures the device, not the caller.

@@ -26,10 +26,13 @@ It restates, in float64 NumPy, the host math of the reference:
   ``kernels.cu:12-87`` (output size, zero padding, dilation; column order
   (c*Kh + kh)*Kw + kw; bias per output channel; dB summed over all images),
   written here as direct sums over the kernel window, not as im2col
+* Elman RNN             -- ``backends/cuda/ops/rnn/launcher.cu:129-383``
+  (h_t = act(X_t Wx + h_{t-1} Wh + b); backward through time with
+  dh_next = dZ_t Wh^T; dB summed over all steps)
 
 Parity pins (what keeps this restatement honest) live in ``tests/test_oracle.py``:
-exact-integer brute force for the GEMMs and the convolution (pure-Python loops), central finite differences for every
-activation derivative and for the backward (a scalar loss), the erf form of GELU
+exact-integer brute force for the GEMMs, the convolution and the RNN recurrence (pure-Python loops), central finite
+differences for every activation derivative and for the GEMM, conv and RNN backwards (a scalar loss), the erf form of GELU
 for the tanh approximation, and the C restatement in ``gemm_oracle.c`` (fp32,
 sequential-k ``fmaf`` -- the reference's own small-kernel order).
 """
@@ -406,3 +409,44 @@ def conv2d_backward(X, W, dY, Z, stride=(1, 1), pad=(0, 0), dil=(1, 1), act="non
                 np.einsum("nohw,oc->nchw", dZ, W[:, :, kh, kw])
     dX = dXp[:, :, pad[0]:pad[0] + H, pad[1]:pad[1] + Wd]
     return {"dZ": dZ, "dW": dW, "dB": dZ.sum(axis=(0, 2, 3)), "dX": dX}
+
+
+def rnn_forward(X, Wx, Wh, h0, bias=None, act="none", slope: float = 0.01) -> Tuple[np.ndarray, np.ndarray]:
+    """h_t = act(X[:,t] Wx + h_{t-1} Wh + b) for t = 0..T-1 from h0 (rnn/launcher.cu:186-227).
+    Returns (Y, Z), float64 [N,T,H]: Y[:,t] = h_t, Z[:,t] = the pre-activation."""
+    X = np.asarray(X, np.float64)
+    Wx, Wh = np.asarray(Wx, np.float64), np.asarray(Wh, np.float64)
+    N, T, _ = X.shape
+    H = Wx.shape[1]
+    b = np.zeros(H) if bias is None else np.asarray(bias, np.float64).reshape(H)
+    Y, Z = np.zeros((N, T, H)), np.zeros((N, T, H))
+    h = np.asarray(h0, np.float64)
+    for t in range(T):
+        Z[:, t] = X[:, t] @ Wx + h @ Wh + b
+        h = act_forward(Z[:, t], act, slope)
+        Y[:, t] = h
+    return Y, Z
+
+
+def rnn_backward(X, Wx, Wh, h0, dY, Z, act="none", slope: float = 0.01) -> dict:
+    """Backward through time (rnn/launcher.cu:300-370): from t = T-1 down to 0,
+    dZ_t = (dY[:,t] + dh_next) * act'(Z[:,t]); dWx += X_t^T dZ_t; dWh += h_{t-1}^T dZ_t
+    (h_{-1} = h0, h_{t-1} = act(Z[:,t-1])); dB += column sums of dZ_t; dX[:,t] = dZ_t Wx^T;
+    dh_next = dZ_t Wh^T; dh0 = the last dh_next.  float64."""
+    X, dY, Z = (np.asarray(a, np.float64) for a in (X, dY, Z))
+    Wx, Wh = np.asarray(Wx, np.float64), np.asarray(Wh, np.float64)
+    h0 = np.asarray(h0, np.float64)
+    N, T, I = X.shape
+    H = Wx.shape[1]
+    dWx, dWh, dB = np.zeros((I, H)), np.zeros((H, H)), np.zeros(H)
+    dX = np.zeros((N, T, I))
+    dh = np.zeros((N, H))
+    for t in range(T - 1, -1, -1):
+        dZ = (dY[:, t] + dh) * act_deriv(Z[:, t], act, slope)
+        hprev = h0 if t == 0 else act_forward(Z[:, t - 1], act, slope)
+        dWx += X[:, t].T @ dZ
+        dWh += hprev.T @ dZ
+        dB += dZ.sum(axis=0)
+        dX[:, t] = dZ @ Wx.T
+        dh = dZ @ Wh.T
+    return {"dWx": dWx, "dWh": dWh, "dB": dB, "dX": dX, "dh0": dh}

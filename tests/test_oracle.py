@@ -430,3 +430,65 @@ def test_conv2d_backward_exact_integers(geom):
     assert np.array_equal(r["dX"], np.array(dX, dtype=np.float64))
     assert np.array_equal(r["dW"], np.array(dW, dtype=np.float64))
     assert np.array_equal(r["dB"], np.array(dB, dtype=np.float64))
+
+
+# ---------------------------------------------------------------------------
+# Elman RNN
+# ---------------------------------------------------------------------------
+def test_rnn_forward_exact_integers():
+    """Pure-Python integer recurrence h_t = X_t Wx + h_{t-1} Wh + b (act none), step by step."""
+    g = np.random.default_rng(41)
+    N, T, I, H = 2, 4, 3, 5
+    X = g.integers(-2, 3, (N, T, I))
+    Wx = g.integers(-1, 2, (I, H))
+    Wh = g.integers(-1, 2, (H, H))
+    h0 = g.integers(-2, 3, (N, H))
+    b = g.integers(-3, 4, H)
+    Y, Z = O.rnn_forward(X, Wx, Wh, h0, b)
+    h = [[int(v) for v in row] for row in h0]
+    for t in range(T):
+        new = [[int(b[j]) + sum(int(X[n, t, i]) * int(Wx[i, j]) for i in range(I))
+                + sum(h[n][k] * int(Wh[k, j]) for k in range(H)) for j in range(H)] for n in range(N)]
+        assert np.array_equal(Z[:, t], np.array(new, dtype=np.float64))
+        h = new
+    assert np.array_equal(Y, Z)
+
+
+def test_rnn_one_step_is_the_concatenated_gemm():
+    """T = 1: act([X_0, h0] [Wx; Wh] + b), the reference's per-step GEMM (launcher.cu:186-205)."""
+    g = np.random.default_rng(43)
+    X, Wx, Wh = g.standard_normal((3, 1, 4)), g.standard_normal((4, 6)), g.standard_normal((6, 6))
+    h0, b = g.standard_normal((3, 6)), g.standard_normal(6)
+    Y, Z = O.rnn_forward(X, Wx, Wh, h0, b, act="tanh")
+    Yg, Zg = O.gemm_forward(np.concatenate([X[:, 0], h0], axis=1), np.concatenate([Wx, Wh]), b, O.BIAS_PERN,
+                            "tanh")
+    assert np.allclose(Z[:, 0], Zg, rtol=1e-12, atol=1e-12) and np.allclose(Y[:, 0], Yg, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("act", ["none", "tanh", "relu", "sigmoid"])
+def test_rnn_backward_matches_finite_difference(act):
+    """d/dX, d/dWx, d/dWh, d/dh0, d/db of L = sum(dY * Y) by central differences: a dropped
+    dh_next term, a wrong h_{t-1} or a transposed weight gradient fails here."""
+    g = np.random.default_rng(45)
+    N, T, I, H = 2, 4, 3, 5
+    X, Wx = g.standard_normal((N, T, I)), 0.5 * g.standard_normal((I, H))
+    Wh, h0, b = 0.5 * g.standard_normal((H, H)), g.standard_normal((N, H)), g.standard_normal(H)
+    _, Z = O.rnn_forward(X, Wx, Wh, h0, b, act=act)
+    dY = g.standard_normal(Z.shape)
+    r = O.rnn_backward(X, Wx, Wh, h0, dY, Z, act=act)
+
+    def loss(X_, Wx_, Wh_, h0_, b_):
+        Y_, _ = O.rnn_forward(X_, Wx_, Wh_, h0_, b_, act=act)
+        return float((dY * Y_).sum())
+
+    args = [X, Wx, Wh, h0, b]
+    h = 1e-6
+    for k, name, idxs in ((0, "dX", [(0, 0, 1), (1, 3, 2), (1, 1, 0)]), (1, "dWx", [(2, 4), (0, 1)]),
+                          (2, "dWh", [(3, 1), (0, 0)]), (3, "dh0", [(1, 2), (0, 4)]), (4, "dB", [(3,)])):
+        for idx in idxs:
+            p, m = [a.copy() for a in args], [a.copy() for a in args]
+            p[k][idx] += h
+            m[k][idx] -= h
+            fd = (loss(*p) - loss(*m)) / (2 * h)
+            # (relu: no pre-activation at this seed lies within h of the kink at 0)
+            assert abs(fd - r[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (act, name, idx, fd, r[name][idx])

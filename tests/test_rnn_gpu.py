@@ -1,0 +1,145 @@
+"""GPU parity of the Elman RNN on the operator (the _ops_rnn module with the reference's
+workspace contract, rnn/launcher.cu:129-383) against the float64 oracle: forward Y / Z and
+the backward through time (dWx, dWh, dB summed over steps, dh0, dX) for every activation,
+batches on the skinny path (N <= 16) and the tile path, exact-integer inputs bit-exact, a
+subset of requested gradients, and bf16 tensors."""
+import numpy as np
+import pytest
+
+from oracle import gemm_oracle as O
+from gemm_helpers import BF16, F32, rounded
+
+pytestmark = pytest.mark.gpu
+
+ACTS = ["none", "relu", "leakyrelu", "gelu", "sigmoid", "tanh"]
+
+
+@pytest.fixture(scope="module")
+def env(gpu):
+    from graph_executor_v2.ops import _ops_rnn as rnn
+    from graph_executor_v2.ops.device_array import DeviceArray
+    return rnn, DeviceArray
+
+
+def _act(rnn, name):
+    return {"none": rnn.ActKind.__members__["None"], "relu": rnn.ActKind.ReLU, "leakyrelu": rnn.ActKind.LeakyReLU,
+            "gelu": rnn.ActKind.GELU, "sigmoid": rnn.ActKind.Sigmoid, "tanh": rnn.ActKind.Tanh}[name]
+
+
+def _run(env, X, Wx, Wh, h0, b, act, dY=None, dtype=F32, want=("dWx", "dWh", "dB", "dh0", "dX")):
+    rnn, DA = env
+    dt = "float32" if dtype == F32 else "bfloat16"
+    cdt = rnn.DType.F32 if dtype == F32 else rnn.DType.BF16
+    N, T, I = X.shape
+    H = Wx.shape[1]
+    gX, gWx, gWh, gh0 = (DA.from_numpy(a, dt) for a in (X, Wx, Wh, h0))
+    gb = DA.from_numpy(b, "float32") if b is not None else None
+    Y, Z = DA.empty((N, T, H), dt), DA.empty((N, T, H), dt)
+    a = rnn.RnnAttrs()
+    a.act, a.with_bias, a.save_z = _act(rnn, act), b is not None, True
+    # the reference's forward workspaces (rnn_pybind.cpp:84-87), kept alive for the call
+    fws = dict(XH_cat_ptr=DA.empty((N, I + H)), Y_rows_ptr=DA.empty((N, H)), W_cat_ptr=DA.empty((I + H, H)),
+               Z_rows_ptr=DA.empty((N, H)))
+    rnn.forward(gX.ptr, list(X.shape), gWx.ptr, list(Wx.shape), gWh.ptr, list(Wh.shape), gh0.ptr, list(h0.shape),
+                Y.ptr, [N, T, H], bias_ptr=gb.ptr if gb is not None else None, z_ptr=Z.ptr, attrs=a, dtype=cdt,
+                **{k: v.ptr for k, v in fws.items()})
+    out = {"Y": Y.get(), "Z": Z.get()}
+    if dY is not None:
+        gdY = DA.from_numpy(dY, dt)
+        grads = {"dWx": DA.empty(Wx.shape, dt), "dWh": DA.empty(Wh.shape, dt), "dB": DA.empty((H,), "float32"),
+                 "dh0": DA.empty(h0.shape, dt), "dX": DA.empty(X.shape, dt)}
+        bws = dict(XH_cat_ptr=DA.empty((N, I + H)), G_rows_ptr=DA.empty((N, H)), Z_rows_ptr=DA.empty((N, H)),
+                   W_cat_ptr=DA.empty((I + H, H)), dXH_cat_ptr=DA.empty((N, I + H)),
+                   dWcat_ptr=DA.empty((I + H, H)), TmpW_ptr=DA.empty((I + H, H)))
+        kw = {k.lower() + "_ptr": (grads[k].ptr if k in want else None) for k in grads}
+        rnn.backward(gX.ptr, list(X.shape), gWx.ptr, list(Wx.shape), gWh.ptr, list(Wh.shape), gh0.ptr,
+                     list(h0.shape), gdY.ptr, [N, T, H], Z.ptr, [N, T, H], attrs=a, dtype=cdt,
+                     **kw, **{k: v.ptr for k, v in bws.items()})
+        out.update({k: grads[k].get() for k in want})
+    return out
+
+
+def _inputs(seed, N, T, I, H):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal((N, T, I)).astype(np.float32),
+            (r.standard_normal((I, H)) / np.sqrt(I)).astype(np.float32),
+            (0.5 * r.standard_normal((H, H)) / np.sqrt(H)).astype(np.float32),
+            r.standard_normal((N, H)).astype(np.float32),
+            (0.1 * r.standard_normal(H)).astype(np.float32),
+            r.standard_normal((N, T, H)).astype(np.float32))
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("shape", [(4, 6, 24, 32), (40, 5, 48, 64)], ids=["skinny-N4", "tile-N40"])
+def test_rnn_f32(env, act, shape):
+    N, T, I, H = shape
+    X, Wx, Wh, h0, b, dY = _inputs(11, N, T, I, H)
+    out = _run(env, X, Wx, Wh, h0, b, act, dY=dY)
+    Y64, Z64 = O.rnn_forward(X, Wx, Wh, h0, b, act)
+    np.testing.assert_allclose(out["Z"], Z64, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(out["Y"], Y64, rtol=1e-4, atol=1e-5)
+    # gradients of the device's own forward (the recurrence re-reads Z)
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, out["Z"].astype(np.float64), act)
+    for k in ("dWx", "dWh", "dB", "dh0", "dX"):
+        np.testing.assert_allclose(out[k], ref[k], rtol=1e-4, atol=1e-4, err_msg=k)
+
+
+def test_rnn_exact_integers(env):
+    """Integer inputs keep every sum exact in fp32: the step order, the h_{t-1} source, the
+    dh_next chain and the per-step sums of dW / dB are checked bit-exact."""
+    r = np.random.default_rng(12)
+    N, T, I, H = 3, 4, 3, 5
+    X = r.integers(-2, 3, (N, T, I)).astype(np.float32)
+    Wx, Wh = (r.integers(-1, 2, s).astype(np.float32) for s in ((I, H), (H, H)))
+    h0 = r.integers(-2, 3, (N, H)).astype(np.float32)
+    b = r.integers(-3, 4, H).astype(np.float32)
+    dY = r.integers(-2, 3, (N, T, H)).astype(np.float32)
+    out = _run(env, X, Wx, Wh, h0, b, "none", dY=dY)
+    Y64, Z64 = O.rnn_forward(X, Wx, Wh, h0, b)
+    assert np.array_equal(out["Z"], Z64) and np.array_equal(out["Y"], Y64)
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, Z64)
+    for k in ("dWx", "dWh", "dB", "dh0", "dX"):
+        assert np.array_equal(out[k], ref[k]), k
+
+
+def test_rnn_subset_of_gradients(env):
+    """Only dWh and dB requested: the others stay untouched, the requested ones are unchanged."""
+    N, T, I, H = 5, 3, 8, 16
+    X, Wx, Wh, h0, b, dY = _inputs(13, N, T, I, H)
+    full = _run(env, X, Wx, Wh, h0, b, "tanh", dY=dY)
+    part = _run(env, X, Wx, Wh, h0, b, "tanh", dY=dY, want=("dWh", "dB"))
+    assert np.array_equal(full["dWh"], part["dWh"]) and np.array_equal(full["dB"], part["dB"])
+
+
+def test_rnn_without_bias(env):
+    N, T, I, H = 4, 3, 8, 16
+    X, Wx, Wh, h0, _, dY = _inputs(14, N, T, I, H)
+    out = _run(env, X, Wx, Wh, h0, None, "relu", dY=dY, want=("dWx", "dWh", "dh0", "dX"))
+    Y64, _ = O.rnn_forward(X, Wx, Wh, h0, None, "relu")
+    np.testing.assert_allclose(out["Y"], Y64, rtol=1e-4, atol=1e-5)
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, out["Z"].astype(np.float64), "relu")
+    for k in ("dWx", "dWh", "dh0", "dX"):
+        np.testing.assert_allclose(out[k], ref[k], rtol=1e-4, atol=1e-4, err_msg=k)
+
+
+@pytest.mark.parametrize("shape", [(8, 6, 32, 64), (40, 4, 64, 128)], ids=["skinny-N8", "tile-N40"])
+def test_rnn_bf16(env, shape):
+    """bf16 tensors (additive): each step rounds h_t and Z_t to bf16, so the comparison is
+    against the oracle fed the device's own Z (one step's error, not T steps compounded),
+    within a few bf16 roundings of the step's magnitude sums."""
+    N, T, I, H = shape
+    X, Wx, Wh, h0, b, dY = _inputs(15, N, T, I, H)
+    X, Wx, Wh, h0, dY = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0, dY))
+    out = _run(env, X, Wx, Wh, h0, b, "tanh", dY=dY, dtype=BF16)
+    Z = out["Z"].astype(np.float64)
+    eps = 2.0 ** -8
+    for t in range(T):
+        hprev = h0 if t == 0 else out["Y"][:, t - 1]
+        zt = X[:, t] @ Wx + hprev @ Wh + b
+        mag = np.abs(X[:, t]) @ np.abs(Wx) + np.abs(hprev) @ np.abs(Wh) + np.abs(b)
+        assert np.all(np.abs(Z[:, t] - zt) <= 2 * eps * mag + 1e-6), t
+        assert np.all(np.abs(out["Y"][:, t] - np.tanh(Z[:, t])) <= 2 * eps * np.abs(np.tanh(Z[:, t])) + 1e-6), t
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, Z, "tanh")
+    for k in ("dWx", "dWh", "dB", "dh0", "dX"):
+        rel = np.abs(out[k] - ref[k]).max() / max(1e-6, np.abs(ref[k]).max())
+        assert rel <= 0.05, (k, rel)
