@@ -30,7 +30,7 @@ INCLUDE = os.path.join(REPO, "include")
 HIP_SOURCES = [
     "gemm_tile_f32.hip", "gemm_tile_bf16.hip", "gemm_tile_f16.hip",
     "gemm_dl_bf16.hip", "gemm_dl_f16.hip",
-    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "rnn.hip", "probe.hip",
+    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "rnn.hip", "attn.hip", "probe.hip",
 ]
 HIP_HEADERS = ["gev2_device.hpp", "gev2_kernels.hpp", "gemm_tile_impl.hpp", "gemm_dl_impl.hpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

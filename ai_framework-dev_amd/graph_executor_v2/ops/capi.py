@@ -29,6 +29,7 @@ EXPORTED = [
     "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16",
     "gev2_conv2d_fwd", "gev2_conv2d_bwd", "gev2_conv2d_last_error",
     "gev2_rnn_fwd", "gev2_rnn_bwd", "gev2_rnn_last_error",
+    "gev2_sdpa_fwd", "gev2_sdpa_bwd", "gev2_sdpa_workspace_size", "gev2_sdpa_last_error",
 ]
 
 
@@ -118,6 +119,27 @@ class RnnBwdDesc(ctypes.Structure):
     ]
 
 
+MASK_NONE, MASK_I8, MASK_I32, MASK_F32 = 0, 1, 2, 3
+_SDPA_HEAD = [("dtype", ctypes.c_int32), ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("M", ctypes.c_int32),
+              ("N", ctypes.c_int32), ("D", ctypes.c_int32), ("scale", ctypes.c_float), ("causal", ctypes.c_int32),
+              ("dropout_p", ctypes.c_float), ("mask_kind", ctypes.c_int32), ("mask", ctypes.c_void_p)]
+
+
+class SdpaDesc(ctypes.Structure):
+    _fields_ = [
+        *_SDPA_HEAD, ("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("Y", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+class SdpaBwdDesc(ctypes.Structure):
+    _fields_ = [
+        *_SDPA_HEAD, ("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("dY", ctypes.c_void_p),
+        ("dQ", ctypes.c_void_p), ("dK", ctypes.c_void_p), ("dV", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -177,6 +199,12 @@ def lib() -> ctypes.CDLL:
     L.gev2_rnn_bwd.argtypes = [ctypes.POINTER(RnnBwdDesc), vp]
     L.gev2_rnn_last_error.restype = ctypes.c_char_p
     L.gev2_rnn_last_error.argtypes = []
+    L.gev2_sdpa_fwd.argtypes = [ctypes.POINTER(SdpaDesc), vp]
+    L.gev2_sdpa_bwd.argtypes = [ctypes.POINTER(SdpaBwdDesc), vp]
+    L.gev2_sdpa_workspace_size.restype = ctypes.c_int64
+    L.gev2_sdpa_workspace_size.argtypes = [ctypes.POINTER(SdpaDesc), ctypes.c_int]
+    L.gev2_sdpa_last_error.restype = ctypes.c_char_p
+    L.gev2_sdpa_last_error.argtypes = []
     _lib = L
     return L
 
@@ -199,6 +227,13 @@ def check_rnn(status: int, where: str) -> None:
     if status != 0:
         L = lib()
         raise GemmError(status, where, (L.gev2_rnn_last_error() or b"").decode()
+                        or L.gev2_status_string(status).decode())
+
+
+def check_sdpa(status: int, where: str) -> None:
+    if status != 0:
+        L = lib()
+        raise GemmError(status, where, (L.gev2_sdpa_last_error() or b"").decode()
                         or L.gev2_status_string(status).decode())
 
 

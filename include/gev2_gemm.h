@@ -283,6 +283,64 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* desc, void* stream);
 const char* gev2_rnn_last_error(void);
 
 /*
+ * Scaled dot-product attention (replaces SDPACudaLaunch /
+ * SDPACudaBackwardLaunch, sdpa/api.hpp:8-33, sdpa/launcher.cu:129-747):
+ *   S = scale * Q K^T (+ masks), P = softmax over keys, Y = P V.
+ * Q [B,H,M,D], K / V [B,H,N,D], Y [B,H,M,D], contiguous, one dtype.
+ * scale 0 means 1/sqrt(D).  causal adds -1e9 where key > query; mask
+ * [B,1,M,N] (broadcast over H): I8 / I32 entries != 0 add -1e9, F32 entries
+ * are added.  dropout_p must be 0 (GEV2_UNIMPLEMENTED otherwise).
+ * F16 / BF16 with D = 64 or 128: one fused kernel, no workspace; `lse`
+ * (optional, fp32 [B,H,M]) receives each row's log-sum-exp.
+ * F32: S / P in `workspace` (gev2_sdpa_workspace_size bytes).
+ */
+enum { GEV2_MASK_NONE = 0, GEV2_MASK_I8 = 1, GEV2_MASK_I32 = 2, GEV2_MASK_F32 = 3 };
+
+typedef struct gev2_sdpa_desc {
+  int32_t dtype;
+  int32_t B, H, M, N, D;
+  float scale;
+  int32_t causal;
+  float dropout_p;
+  int32_t mask_kind;               /* GEV2_MASK_* */
+  const void* mask;
+  const void* Q;
+  const void* K;
+  const void* V;
+  void* Y;
+  float* lse;
+  void* workspace;  int64_t workspace_bytes;
+} gev2_sdpa_desc;
+
+/* dQ / dK / dV (each optional, not all NULL) of the forward above for dY. */
+typedef struct gev2_sdpa_bwd_desc {
+  int32_t dtype;
+  int32_t B, H, M, N, D;
+  float scale;
+  int32_t causal;
+  float dropout_p;
+  int32_t mask_kind;
+  const void* mask;
+  const void* Q;
+  const void* K;
+  const void* V;
+  const void* dY;
+  void* dQ;
+  void* dK;
+  void* dV;
+  void* workspace;  int64_t workspace_bytes;
+} gev2_sdpa_bwd_desc;
+
+int gev2_sdpa_fwd(const gev2_sdpa_desc* desc, void* stream);
+int gev2_sdpa_bwd(const gev2_sdpa_bwd_desc* desc, void* stream);
+/* Workspace bytes of the forward (backward != 0: of the backward) for these
+ * dimensions and dtype; -1 for an invalid descriptor.  No counterpart in the
+ * reference, which allocates its S / P buffers on every call. */
+int64_t gev2_sdpa_workspace_size(const gev2_sdpa_desc* desc, int backward);
+/* Message for the last failing attention call on this thread ("" if none). */
+const char* gev2_sdpa_last_error(void);
+
+/*
  * Benchmark helpers (no counterpart in the reference): issue `reps` calls back
  * to back on `stream`, call i using descs[i % n_descs] (rotating buffer sets),
  * so that a timing of small problems measures the device, not the caller.

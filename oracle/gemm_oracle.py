@@ -26,6 +26,11 @@ It restates, in float64 NumPy, the host math of the reference:
   ``kernels.cu:12-87`` (output size, zero padding, dilation; column order
   (c*Kh + kh)*Kw + kw; bias per output channel; dB summed over all images),
   written here as direct sums over the kernel window, not as im2col
+* attention (SDPA)      -- ``backends/cuda/ops/sdpa/launcher.cu:129-747``
+  (S = scale Q K^T, scale 0 -> 1/sqrt(D); external mask [B,1,M,N] then causal,
+  each adding -1e9 in fp32 (F32 masks add their value); softmax over keys;
+  Y = P V; backward dV = P^T dY, dS = P (dP - rowsum(dP P)) zeroed where
+  masked, dQ = scale dS K, dK = scale dS^T Q)
 * Elman RNN             -- ``backends/cuda/ops/rnn/launcher.cu:129-383``
   (h_t = act(X_t Wx + h_{t-1} Wh + b); backward through time with
   dh_next = dZ_t Wh^T; dB summed over all steps)
@@ -450,3 +455,67 @@ def rnn_backward(X, Wx, Wh, h0, dY, Z, act="none", slope: float = 0.01) -> dict:
         dX[:, t] = dZ @ Wx.T
         dh = dZ @ Wh.T
     return {"dWx": dWx, "dWh": dWh, "dB": dB, "dX": dX, "dh0": dh}
+
+
+MASK_NONE, MASK_I8, MASK_I32, MASK_F32 = 0, 1, 2, 3
+
+
+def _sdpa_scores(Q, K, scale, causal, mask, mask_kind):
+    """Scaled scores with the masks of launcher.cu:179-215 (external mask, then causal).  A
+    masked entry is formed as the reference forms it, by an fp32 addition of -1e9 (or of the
+    F32 mask value) to the fp32-rounded score; unmasked entries stay float64."""
+    Q, K = np.asarray(Q, np.float64), np.asarray(K, np.float64)
+    S = np.einsum("bhmd,bhnd->bhmn", Q, K) * scale
+    M, N = S.shape[2], S.shape[3]
+    add = np.zeros(S.shape, np.float32)
+    hit = np.zeros(S.shape, bool)
+    if mask_kind != MASK_NONE:
+        mk = np.asarray(mask)[:, :1]                     # [B,1,M,N], broadcast over H
+        if mask_kind == MASK_F32:
+            add = add + mk.astype(np.float32)
+            hit = hit | (mk != 0)
+        else:
+            add = add + np.where(mk != 0, np.float32(-1e9), np.float32(0))
+            hit = hit | (mk != 0)
+    if causal:
+        cm = np.triu(np.ones((M, N), bool), 1)
+        hit = hit | cm
+    out = S.copy()
+    if hit.any():
+        s32 = S.astype(np.float32)
+        if mask_kind != MASK_NONE:
+            s32 = (s32 + np.broadcast_to(add, S.shape)).astype(np.float32)
+        if causal:
+            s32 = np.where(np.triu(np.ones((M, N), bool), 1), (s32 + np.float32(-1e9)).astype(np.float32), s32)
+        out = np.where(hit, s32.astype(np.float64), S)
+    return out, np.broadcast_to(hit, S.shape)
+
+
+def sdpa_forward(Q, K, V, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE):
+    """Y = softmax(scale Q K^T + masks) V over [B,H,M,N] (launcher.cu:129-274).
+    Returns (Y, P, lse) in float64; lse = log sum exp of the masked scaled scores per row."""
+    D = np.asarray(Q).shape[-1]
+    sc = scale if scale != 0.0 else 1.0 / math.sqrt(D)
+    S, _ = _sdpa_scores(Q, K, sc, causal, mask, mask_kind)
+    mx = S.max(axis=-1, keepdims=True)
+    E = np.exp(S - mx)
+    l = E.sum(axis=-1, keepdims=True)
+    P = E / l
+    Y = np.einsum("bhmn,bhnd->bhmd", P, np.asarray(V, np.float64))
+    return Y, P, (mx + np.log(l))[..., 0]
+
+
+def sdpa_backward(Q, K, V, dY, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE):
+    """dQ, dK, dV of sdpa_forward for upstream dY (launcher.cu:333-747), float64."""
+    Q, K, V, dY = (np.asarray(a, np.float64) for a in (Q, K, V, dY))
+    D = Q.shape[-1]
+    sc = scale if scale != 0.0 else 1.0 / math.sqrt(D)
+    _, P, _ = sdpa_forward(Q, K, V, scale, causal, mask, mask_kind)
+    _, hit = _sdpa_scores(Q, K, sc, causal, mask, mask_kind)
+    dV = np.einsum("bhmn,bhmd->bhnd", P, dY)
+    dP = np.einsum("bhmd,bhnd->bhmn", dY, V)
+    dS = P * (dP - (dP * P).sum(axis=-1, keepdims=True))
+    dS = np.where(hit, 0.0, dS)
+    dQ = sc * np.einsum("bhmn,bhnd->bhmd", dS, K)
+    dK = sc * np.einsum("bhmn,bhmd->bhnd", dS, Q)
+    return {"dQ": dQ, "dK": dK, "dV": dV}

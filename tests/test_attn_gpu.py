@@ -1,0 +1,141 @@
+"""GPU parity of scaled dot-product attention through the C ABI (gev2_sdpa_fwd / _bwd,
+the sdpa op of sdpa/launcher.cu:129-747) against the float64 oracle:
+  - the fused 16-bit kernel (bf16 / fp16, D = 64 and 128) with ragged M / N, causal and the
+    three external mask kinds, and its row log-sum-exp;
+  - the fp32 path (the reference's type) forward and backward, with the same masks;
+  - the reference's validation results (dropout, all-null outputs)."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from oracle import gemm_oracle as O
+from gemm_helpers import BF16, F16, F32, rounded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def capi(gpu):
+    from graph_executor_v2.ops import capi as c
+    return c
+
+
+def _mask(kind, B, M, N, seed):
+    if kind == O.MASK_NONE:
+        return None
+    r = np.random.default_rng(seed)
+    hit = r.random((B, 1, M, N)) < 0.25
+    hit[..., 0] = False                         # every row keeps a key
+    if kind == O.MASK_I8:
+        return hit.astype(np.int8)
+    if kind == O.MASK_I32:
+        return hit.astype(np.int32)
+    return np.where(hit, -2.5, 0.0).astype(np.float32)
+
+
+def _fwd(capi, Q, K, V, dtype, causal=False, mask=None, mask_kind=O.MASK_NONE, scale=0.0, want_lse=True):
+    B, H, M, D = Q.shape
+    N = K.shape[2]
+    bufs = [capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype)) for a in (Q, K, V)]
+    es = capi.elem_bytes(dtype)
+    Y = capi.DeviceBuffer(B * H * M * D * es)
+    lse = capi.DeviceBuffer(B * H * M * 4) if want_lse else None
+    mk = capi.DeviceBuffer.from_numpy(mask) if mask is not None else None
+    d = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, scale=scale, causal=int(causal), mask_kind=mask_kind,
+                      mask=mk.ptr if mk else None, Q=bufs[0].ptr, K=bufs[1].ptr, V=bufs[2].ptr, Y=Y.ptr,
+                      lse=lse.ptr if lse else None)
+    L = capi.lib()
+    wsb = L.gev2_sdpa_workspace_size(ctypes.byref(d), 0)
+    ws = capi.DeviceBuffer(max(wsb, 1)) if wsb > 0 else None
+    if ws:
+        d.workspace, d.workspace_bytes = ws.ptr, wsb
+    capi.check_sdpa(L.gev2_sdpa_fwd(ctypes.byref(d), None), "sdpa fwd")
+    capi.synchronize()
+    y = capi.from_storage(Y.download((B, H, M, D), capi.to_storage(np.zeros(1, np.float32), dtype).dtype), dtype)
+    return y, (lse.download((B, H, M), np.float32) if lse else None)
+
+
+def _qkv(seed, B, H, M, N, D, dtype):
+    r = np.random.default_rng(seed)
+    Q, K, V = (r.standard_normal(s).astype(np.float32) for s in ((B, H, M, D), (B, H, N, D), (B, H, N, D)))
+    if dtype != F32:
+        Q, K, V = (rounded(a, dtype).astype(np.float32) for a in (Q, K, V))
+    return Q, K, V
+
+
+FUSED_CASES = [
+    # (B, H, M, N, D, causal, mask kind)
+    (2, 3, 200, 136, 64, False, O.MASK_NONE),
+    (1, 2, 128, 256, 128, False, O.MASK_NONE),
+    (2, 2, 192, 192, 64, True, O.MASK_NONE),
+    (1, 3, 70, 100, 64, False, O.MASK_I8),
+    (2, 1, 130, 64, 128, True, O.MASK_I32),
+    (1, 2, 96, 160, 64, False, O.MASK_F32),
+]
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "B{}H{}M{}N{}D{}{}{}".format(
+    *c[:5], "-causal" if c[5] else "", ["", "-i8", "-i32", "-f32"][c[6]]))
+def test_fused_forward(capi, dtype, case):
+    """Per element: |Y - Y64| <= 2 eps (P |V|) + 1e-4, eps the storage epsilon (P is rounded
+    to the storage type for the P V product); lse within 1e-4 (1 + |lse|)."""
+    B, H, M, N, D, causal, mk = case
+    Q, K, V = _qkv(21, B, H, M, N, D, dtype)
+    mask = _mask(mk, B, M, N, 22)
+    y, lse = _fwd(capi, Q, K, V, dtype, causal, mask, mk)
+    Y64, P64, lse64 = O.sdpa_forward(Q, K, V, causal=causal, mask=mask, mask_kind=mk)
+    eps = O.storage_eps(dtype)
+    bound = 2 * eps * np.einsum("bhmn,bhnd->bhmd", P64, np.abs(V)) + 1e-4 + eps * np.abs(Y64)
+    err = np.abs(y - Y64)
+    assert np.all(err <= bound), (float(err.max()), np.unravel_index(int(np.argmax(err - bound)), err.shape))
+    assert np.all(np.abs(lse - lse64) <= 1e-4 * (1 + np.abs(lse64)))
+
+
+def test_fused_forward_scale_attr(capi):
+    """attrs.scale overrides 1/sqrt(D)."""
+    Q, K, V = _qkv(23, 1, 2, 64, 64, 64, BF16)
+    y, _ = _fwd(capi, Q, K, V, BF16, scale=0.3)
+    Y64, P64, _ = O.sdpa_forward(Q, K, V, scale=0.3)
+    eps = O.storage_eps(BF16)
+    assert np.all(np.abs(y - Y64) <= 2 * eps * np.einsum("bhmn,bhnd->bhmd", P64, np.abs(V)) + 1e-4 + eps * np.abs(Y64))
+
+
+@pytest.mark.parametrize("causal,mk", [(False, O.MASK_NONE), (True, O.MASK_NONE), (False, O.MASK_I8),
+                                       (True, O.MASK_F32)], ids=["plain", "causal", "i8", "causal-f32"])
+def test_f32_forward_backward(capi, causal, mk):
+    B, H, M, N, D = 2, 2, 48, 40, 16
+    Q, K, V = _qkv(24, B, H, M, N, D, F32)
+    mask = _mask(mk, B, M, N, 25)
+    y, _ = _fwd(capi, Q, K, V, F32, causal, mask, mk, want_lse=False)
+    Y64, _, _ = O.sdpa_forward(Q, K, V, causal=causal, mask=mask, mask_kind=mk)
+    np.testing.assert_allclose(y, Y64, rtol=1e-4, atol=1e-5)
+    dY = np.random.default_rng(26).standard_normal(Q.shape).astype(np.float32)
+    bufs = [capi.DeviceBuffer.from_numpy(a) for a in (Q, K, V, dY)]
+    outs = [capi.DeviceBuffer(a.nbytes) for a in (Q, K, V)]
+    mkb = capi.DeviceBuffer.from_numpy(mask) if mask is not None else None
+    d = capi.SdpaBwdDesc(dtype=F32, B=B, H=H, M=M, N=N, D=D, causal=int(causal), mask_kind=mk,
+                         mask=mkb.ptr if mkb else None, Q=bufs[0].ptr, K=bufs[1].ptr, V=bufs[2].ptr, dY=bufs[3].ptr,
+                         dQ=outs[0].ptr, dK=outs[1].ptr, dV=outs[2].ptr)
+    L = capi.lib()
+    fd = capi.SdpaDesc(dtype=F32, B=B, H=H, M=M, N=N, D=D)
+    wsb = L.gev2_sdpa_workspace_size(ctypes.byref(fd), 1)
+    ws = capi.DeviceBuffer(wsb)
+    d.workspace, d.workspace_bytes = ws.ptr, wsb
+    capi.check_sdpa(L.gev2_sdpa_bwd(ctypes.byref(d), None), "sdpa bwd")
+    capi.synchronize()
+    ref = O.sdpa_backward(Q, K, V, dY, causal=causal, mask=mask, mask_kind=mk)
+    for name, buf, a in zip(("dQ", "dK", "dV"), outs, (Q, K, V)):
+        np.testing.assert_allclose(buf.download(a.shape, np.float32), ref[name], rtol=1e-4, atol=1e-4, err_msg=name)
+
+
+def test_validation(capi):
+    L = capi.lib()
+    d = capi.SdpaDesc(dtype=BF16, B=1, H=1, M=8, N=8, D=64, dropout_p=0.1, Q=16, K=32, V=48, Y=64)
+    assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 2            # Unimplemented (dropout)
+    d.dropout_p, d.mask_kind = 0.0, O.MASK_I8
+    assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 10           # mask kind without a mask
+    b = capi.SdpaBwdDesc(dtype=F32, B=1, H=1, M=8, N=8, D=16, Q=16, K=32, V=48, dY=64)
+    assert L.gev2_sdpa_bwd(ctypes.byref(b), None) == 1            # all outputs null (launcher.cu:342)

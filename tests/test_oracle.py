@@ -492,3 +492,71 @@ def test_rnn_backward_matches_finite_difference(act):
             fd = (loss(*p) - loss(*m)) / (2 * h)
             # (relu: no pre-activation at this seed lies within h of the kink at 0)
             assert abs(fd - r[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (act, name, idx, fd, r[name][idx])
+
+
+# ---------------------------------------------------------------------------
+# Scaled dot-product attention
+# ---------------------------------------------------------------------------
+def _qkv(seed, B=2, H=2, M=5, N=7, D=4):
+    g = np.random.default_rng(seed)
+    return g.standard_normal((B, H, M, D)), g.standard_normal((B, H, N, D)), g.standard_normal((B, H, N, D))
+
+
+def test_sdpa_special_cases():
+    Q, K, V = _qkv(51)
+    # one key: softmax of a single score is 1, so Y is that key's value row
+    Y, _, lse = O.sdpa_forward(Q, K[:, :, :1], V[:, :, :1])
+    assert np.allclose(Y, np.broadcast_to(V[:, :, :1], Y.shape), atol=1e-12)
+    # Q = 0: every score equal, so Y is the mean of the value rows and lse = log N
+    Y, _, lse = O.sdpa_forward(np.zeros_like(Q), K, V)
+    assert np.allclose(Y, np.broadcast_to(V.mean(axis=2, keepdims=True), Y.shape), atol=1e-12)
+    assert np.allclose(lse, math.log(7), atol=1e-12)
+    # causal: query 0 sees key 0 only
+    Y, _, _ = O.sdpa_forward(Q, K, V, causal=True)
+    assert np.allclose(Y[:, :, 0], V[:, :, 0], atol=1e-9)
+    # a very large scale turns the softmax into an argmax
+    Y, _, _ = O.sdpa_forward(Q, K, V, scale=1e4)
+    idx = np.argmax(np.einsum("bhmd,bhnd->bhmn", Q, K), axis=-1)
+    assert np.allclose(Y, np.take_along_axis(V, idx[..., None].repeat(4, -1), axis=2), atol=1e-6)
+
+
+def test_sdpa_key_permutation_and_masks():
+    Q, K, V = _qkv(53)
+    perm = np.random.default_rng(1).permutation(7)
+    Y, _, _ = O.sdpa_forward(Q, K, V)
+    Yp, _, _ = O.sdpa_forward(Q, K[:, :, perm], V[:, :, perm])
+    assert np.allclose(Y, Yp, atol=1e-12)
+    # an I8 mask that drops keys equals attention over the kept keys only
+    keep = np.array([1, 0, 1, 1, 0, 1, 1], bool)
+    mask = np.broadcast_to(~keep, (2, 1, 5, 7)).astype(np.int8)
+    Ym, _, _ = O.sdpa_forward(Q, K, V, mask=mask, mask_kind=O.MASK_I8)
+    Yk, _, _ = O.sdpa_forward(Q, K[:, :, keep], V[:, :, keep], scale=1 / math.sqrt(4))
+    assert np.allclose(Ym, Yk, atol=1e-12)
+    # a constant F32 mask shifts every score of a row equally, which the softmax ignores
+    Yc, _, _ = O.sdpa_forward(Q, K, V, mask=np.full((2, 1, 5, 7), 3.0, np.float32), mask_kind=O.MASK_F32)
+    assert np.allclose(Yc, Y, atol=1e-5)
+
+
+@pytest.mark.parametrize("causal,mk", [(False, O.MASK_NONE), (True, O.MASK_NONE), (False, O.MASK_I8)])
+def test_sdpa_backward_matches_finite_difference(causal, mk):
+    Q, K, V = _qkv(55)
+    mask = None
+    if mk == O.MASK_I8:
+        mask = (np.random.default_rng(2).random((2, 1, 5, 7)) < 0.3).astype(np.int8)
+        mask[..., 0] = 0
+    dY = np.random.default_rng(3).standard_normal(Q.shape)
+    r = O.sdpa_backward(Q, K, V, dY, causal=causal, mask=mask, mask_kind=mk)
+
+    def loss(Q_, K_, V_):
+        return float((dY * O.sdpa_forward(Q_, K_, V_, causal=causal, mask=mask, mask_kind=mk)[0]).sum())
+
+    args = [Q, K, V]
+    h = 1e-6
+    for k, name, idxs in ((0, "dQ", [(0, 1, 2, 3), (1, 0, 4, 0)]), (1, "dK", [(0, 0, 6, 1), (1, 1, 2, 2)]),
+                          (2, "dV", [(1, 0, 3, 3), (0, 1, 0, 0)])):
+        for idx in idxs:
+            p, m = [a.copy() for a in args], [a.copy() for a in args]
+            p[k][idx] += h
+            m[k][idx] -= h
+            fd = (loss(*p) - loss(*m)) / (2 * h)
+            assert abs(fd - r[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (name, idx, fd, r[name][idx])
