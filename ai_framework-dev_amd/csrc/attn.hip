@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/gev2_gemm.h"
@@ -34,7 +35,8 @@
 namespace gev2 {
 
 constexpr float kMaskNeg = -1e9f;          // launcher.cu:152
-constexpr int kAttnQ = 128;                // queries per workgroup (32 per wave)
+// queries per wave: 16 * QT (QT = 1 or 2); a workgroup has 4 waves
+__host__ __device__ constexpr int attn_wg_queries(int qt) { return 64 * qt; }
 constexpr int kAttnKeys = 64;              // keys per block
 
 struct AttnArgs {
@@ -48,7 +50,7 @@ struct AttnArgs {
   int BH, H, M, N;
   float scale;
   int causal;
-  int qblocks;           // ceil(M / kAttnQ)
+  int qblocks;           // ceil(M / attn_wg_queries(QT))
 };
 
 // Mask term added to a scaled score (the reference adds the external mask,
@@ -116,8 +118,13 @@ __device__ __forceinline__ void load_kv(const i32x4_t& rK, const i32x4_t& rV, in
   }
 }
 
-template <typename T, int D>
+// MASKED: causal and / or an external mask, or a scale <= 0 (scores formed as
+// the reference forms them: scale, then the fp32 mask additions).  Otherwise
+// the row maximum is taken over the raw dot products and scale * log2(e)
+// enters through the exponent's FMA.  Maxima are kept in base-2 units.
+template <typename T, int D, bool MASKED, int QT>
 __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
+  constexpr int kWgQ = attn_wg_queries(QT);
   using B = KvBlock<D>;
   constexpr int KS = D / 32;                 // k-steps of the S^T product
   constexpr int DT = D / 16;                 // 16-row tiles of O^T
@@ -137,12 +144,12 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   const int b = bh / a.H;
   const int64_t qhead = (int64_t)bh * a.M, khead = (int64_t)bh * a.N;
 
-  // this lane's two query columns; Q rows as B operands (k = d 32s + 8g ..)
-  int q[2];
-  u32x4 qf[2][KS];
+  // this lane's query columns; Q rows as B operands (k = d 32s + 8g ..)
+  int q[QT];
+  u32x4 qf[QT][KS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    q[qt] = qb * kAttnQ + wave * 32 + qt * 16 + col;
+  for (int qt = 0; qt < QT; ++qt) {
+    q[qt] = qb * kWgQ + wave * 16 * QT + qt * 16 + col;
     const T* qrow = static_cast<const T*>(a.Q) + (qhead + q[qt]) * D;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
@@ -154,23 +161,25 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   int nkb = (a.N + kAttnKeys - 1) / kAttnKeys;
   if (a.causal && a.mask_kind == GEV2_MASK_NONE) {
     // blocks whose every key is past every query here add exp(-1e9 + ...) = 0
-    nkb = min(nkb, (qb * kAttnQ + kAttnQ - 1) / kAttnKeys + 1);
+    nkb = min(nkb, (qb * kWgQ + kWgQ - 1) / kAttnKeys + 1);
   }
   const i32x4_t rK = rsrc_words(a.K), rV = rsrc_words(a.V);
   const uint32_t base = lds_addr(&lds[0][0][0]);
   auto k_lds = [&](int st) { return base + st * 2 * B::kBytes; };
   auto v_lds = [&](int st) { return base + st * 2 * B::kBytes + B::kBytes; };
 
-  float m_run[2], l_run[2];
-  f32x4_t o[2][DT];
+  float m_run[QT], l_run[QT];
+  f32x4_t o[QT][DT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     m_run[qt] = -INFINITY;
     l_run[qt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const float kLog2e = 1.4426950408889634f;
+  // base-2 units throughout: x2 = score * log2(e), m in the same units
+  const float xscale = a.scale * kLog2e;
 
   load_kv<D>(rK, rV, khead, 0, a.N, wave, lane, k_lds(0), v_lds(0));
   for (int kb = 0; kb < nkb; ++kb) {
@@ -185,62 +194,82 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
     asm volatile("" ::: "memory");
     const char* kl = &lds[st][0][0];
     const char* vl = &lds[st][1][0];
+    const bool tail = (kb + 1) * kAttnKeys > a.N;
 
     // S^T tiles: s[qt][kt] rows = keys 16 kt + 4 g + r, column = query q[qt]
-    f32x4_t s[2][4];
+    f32x4_t s[QT][4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       const int row = 16 * kt + col;
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int qt = 0; qt < QT; ++qt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int c = (4 * ks + g) ^ (row & 7);
         const u32x4 kf = *reinterpret_cast<const u32x4*>(kl + row * B::kRowBytes + c * 16);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_16x16x32<T>(kf, qf[qt][ks], s[qt][kt]);
+        for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma_16x16x32<T>(kf, qf[qt][ks], s[qt][kt]);
       }
     }
 
     // online softmax; P^T packed as the B operand of O^T += V^T P^T
-    u32x4 pf[2][2];
+    u32x4 pf[QT][2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
+      // x = the score in base-2 units: MASKED forms it as the reference does
+      // (scale, then the fp32 mask additions); otherwise the scale (> 0) is
+      // applied inside the exponent's FMA and the maximum taken over raw dots
       float x[4][4];
       float mloc = -INFINITY;
+      const int key0 = kb * kAttnKeys + 4 * g;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = kb * kAttnKeys + 16 * kt + 4 * g + r;
-          float v = s[qt][kt][r] * a.scale;
-          if (key >= a.N) v = -INFINITY;      // past the last key (zero-filled rows)
-          else if (a.mask_kind != GEV2_MASK_NONE || a.causal) v = mask_add(v, a, b, min(q[qt], a.M - 1), key);
+          float v = s[qt][kt][r];
+          if constexpr (MASKED) {
+            const int key = key0 + 16 * kt + r;
+            v = key < a.N ? mask_add(v * a.scale, a, b, min(q[qt], a.M - 1), key) * kLog2e : -INFINITY;
+          }
           x[kt][r] = v;
-          mloc = fmaxf(mloc, v);
         }
       }
+      if (!MASKED && tail) {
+        // past the last key (zero-filled rows): out of the softmax
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) x[kt][r] = key0 + 16 * kt + r < a.N ? x[kt][r] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) mloc = fmaxf(mloc, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
       mloc = xor_max(xor_max(mloc, 16), 32);
+      if constexpr (!MASKED) mloc *= xscale;
       const float m_new = fmaxf(m_run[qt], mloc);
-      const float corr = exp2f((m_run[qt] - m_new) * kLog2e);
+      // raw v_exp_f32: every argument here is <= 0, so no range fix-up is needed
+      const float corr = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+      const bool grew = m_new > m_run[qt];
       m_run[qt] = m_new;
-      const float mb = m_new * kLog2e;
       float lsum = 0.f;
       uint32_t pb[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = exp2f(fmaf(x[kt][r], kLog2e, -mb));
+          const float arg = MASKED ? x[kt][r] - m_new : fmaf(x[kt][r], xscale, -m_new);
+          const float p = __builtin_amdgcn_exp2f(arg);
           lsum += p;
           pb[kt][r] = Elem<T>::bits(p);
         }
       }
       l_run[qt] = l_run[qt] * corr + lsum;
+      if (__any(grew)) {                      // rescale only when some row's maximum moved
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[qt][dt][r] *= corr;
+          for (int r = 0; r < 4; ++r) o[qt][dt][r] *= corr;
+        }
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -270,7 +299,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
           vf[2 * h + 1] = w2[1];
         }
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma_16x16x32<T>(vf, pf[qt][j], o[qt][dt]);
+        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = mfma_16x16x32<T>(vf, pf[qt][j], o[qt][dt]);
       }
     }
     __syncthreads();                          // stage st is free for block kb + 2
@@ -278,7 +307,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
 
   // Y[q][16 dt + 4 g + r] = O^T / l; 8-byte stores
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const float l = xor_sum(xor_sum(l_run[qt], 16), 32);
     if (q[qt] >= a.M) continue;
     const float inv = 1.f / l;
@@ -290,15 +319,32 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
       w[1] = pack2(Elem<T>::bits(o[qt][dt][2] * inv), Elem<T>::bits(o[qt][dt][3] * inv));
       *reinterpret_cast<u32x2*>(yrow + 16 * dt + 4 * g) = w;
     }
-    if (a.lse && g == 0) a.lse[qhead + q[qt]] = m_run[qt] + logf(l);
+    if (a.lse && g == 0) a.lse[qhead + q[qt]] = (m_run[qt] + log2f(l)) * 0.69314718055994531f;
   }
 }
 
+template <typename T, int D, int QT>
+hipError_t launch_attn_fwd_qt(AttnArgs a, hipStream_t s) {
+  a.qblocks = (a.M + attn_wg_queries(QT) - 1) / attn_wg_queries(QT);
+  const int64_t blocks = (int64_t)a.BH * a.qblocks;
+  if (a.causal || a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f))
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true, QT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false, QT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// 32 queries per wave reuse each K / V fragment read twice; 16 per wave give
+// twice the waves.  The second is taken when the first would leave CUs with
+// fewer than two workgroups (one wave per SIMD cannot overlap the MFMA and
+// softmax phases of a block).
 template <typename T, int D>
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
-  const int64_t blocks = (int64_t)a.BH * a.qblocks;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
-  return hipGetLastError();
+  const int64_t wg2 = (int64_t)a.BH * ((a.M + attn_wg_queries(2) - 1) / attn_wg_queries(2));
+  const char* env = std::getenv("GEV2_ATTN_QT");        // 1 or 2 forces a variant (tuning runs)
+  const int forced = env ? std::atoi(env) : 0;
+  if (forced == 2 || (forced != 1 && wg2 >= 512)) return launch_attn_fwd_qt<T, D, 2>(a, s);
+  return launch_attn_fwd_qt<T, D, 1>(a, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -400,7 +446,6 @@ int attn_check(const Desc* d, gev2::AttnArgs* a) {
   a->causal = d->causal ? 1 : 0;
   a->mask = d->mask;
   a->mask_kind = d->mask_kind;
-  a->qblocks = (d->M + gev2::kAttnQ - 1) / gev2::kAttnQ;
   return GEV2_OK;
 }
 

@@ -330,6 +330,38 @@ def rnn_op_cfg(ctx, dtype, iters, N=8, T=32, I=512, H=1024):
             "fwd_us_per_step": fwd_ms * 1e3 / T, "bwd_us_per_step": bwd_ms * 1e3 / T}
 
 
+def attn_cfg(ctx, dtype, iters, B=8, H=8, M=512, N=512, D=64, causal=False, sets=8):
+    """C4 shape through the attention entry point (gev2_sdpa_fwd): fused kernel for 16-bit
+    tensors (S and P never leave the chip), the batched fp32 path otherwise; `sets` buffer sets
+    rotate so that the MALL does not hold the inputs between launches."""
+    capi = ctx.capi
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(58)
+    L = capi.lib()
+    descs = []
+    for _ in range(sets):
+        Q, K, V = (capi.to_storage(normal(g, s), dtype) for s in ((B, H, M, D), (B, H, N, D), (B, H, N, D)))
+        d = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal), Q=ctx.put(Q), K=ctx.put(K),
+                          V=ctx.put(V), Y=ctx.empty(B * H * M * D * es), lse=ctx.empty(B * H * M * 4))
+        wsb = L.gev2_sdpa_workspace_size(ctypes.byref(d), 0)
+        if wsb > 0:
+            d.workspace, d.workspace_bytes = ctx.empty(wsb), wsb
+            d.lse = None
+        descs.append(d)
+    it = [0]
+
+    def fwd():
+        d = descs[it[0] % sets]
+        it[0] += 1
+        capi.check_sdpa(L.gev2_sdpa_fwd(ctypes.byref(d), ctx.stream.ptr), "sdpa fwd")
+
+    ms = ctx.time_ms(fwd, iters)
+    flop = 4.0 * B * H * M * N * D * (0.5 if causal else 1.0)
+    byt = (B * H * (M + 2 * N) * D + B * H * M * D) * es + B * H * M * 4
+    return {"shape": f"B={B} H={H} M={M} N={N} D={D}" + (" causal" if causal else ""), "fwd_us": ms * 1e3,
+            "tflops": flop / (ms * 1e-3) / 1e12, "gbps_algorithmic": byt / (ms * 1e-3) / 1e9}
+
+
 def skinny_cfg(ctx, iters, sets=10):
     """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL.
     The split-K partials go to a caller workspace (gev2_gemm_fwd_workspace_size)."""
@@ -446,6 +478,9 @@ def main():
             ("c2_f32_1024_gelu", lambda: fp32_cfg(ctx, 1024, 1024, 1024, "gelu", 50, 2)),
             ("c3_f16_4096_relu", lambda: headline(ctx, 10, 3, capi.F16)),
             ("c4_sdpa_bf16", lambda: sdpa_cfg(ctx, capi.BF16, 50)),
+            ("c4_attn_fused_bf16", lambda: attn_cfg(ctx, capi.BF16, 50)),
+            ("c4_attn_fused_bf16_causal", lambda: attn_cfg(ctx, capi.BF16, 50, causal=True)),
+            ("c4_attn_f32", lambda: attn_cfg(ctx, capi.F32, 10, sets=2)),
             ("c5a_conv_f32", lambda: conv_cfg(ctx, capi.F32, 20)),
             ("c5a_conv_bf16", lambda: conv_cfg(ctx, capi.BF16, 20)),
             ("c5a_conv2d_op_f32_per_image", lambda: conv_op_cfg(ctx, capi.F32, 5, 1)),
