@@ -37,7 +37,7 @@ namespace gev2 {
 constexpr float kMaskNeg = -1e9f;          // launcher.cu:152
 // queries per wave: 16 * QT (QT = 1 or 2); a workgroup has 4 waves
 __host__ __device__ constexpr int attn_wg_queries(int qt) { return 64 * qt; }
-constexpr int kAttnKeys = 64;              // keys per block
+// keys per block: 16 * KT (KT = 4 or 8)
 
 struct AttnArgs {
   const void* Q;
@@ -88,19 +88,20 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo 
 // LDS image of one key block: K rows with 16-byte chunks XOR-swizzled by
 // (row & 7) (rows read whole for the A operand), V rows with 32-byte blocks
 // XOR-swizzled by (row & 3) (read with transpose reads).
-template <int D>
+template <int D, int KT>
 struct KvBlock {
+  static constexpr int kKeys = 16 * KT;
   static constexpr int kRowBytes = D * 2;
-  static constexpr int kBytes = kAttnKeys * kRowBytes;        // one of K or V
+  static constexpr int kBytes = kKeys * kRowBytes;            // one of K or V
   static constexpr int kLoadsPerWave = kBytes / 1024 / 4;     // 1 KB loads, 4 waves
   static constexpr int kChunks = D / 8;                       // 16-byte chunks per row
 };
 
-// Issue this wave's direct-to-LDS loads of K and V rows [key0, key0 + 64).
-template <int D>
+// Issue this wave's direct-to-LDS loads of K and V rows [key0, key0 + 16 KT).
+template <int D, int KT>
 __device__ __forceinline__ void load_kv(const i32x4_t& rK, const i32x4_t& rV, int64_t head_off, int key0, int N,
                                         int wave, int lane, uint32_t k_lds, uint32_t v_lds) {
-  using B = KvBlock<D>;
+  using B = KvBlock<D, KT>;
   constexpr int rows_per_load = 1024 / B::kRowBytes;
 #pragma unroll
   for (int j = 0; j < B::kLoadsPerWave; ++j) {
@@ -122,10 +123,15 @@ __device__ __forceinline__ void load_kv(const i32x4_t& rK, const i32x4_t& rV, in
 // the reference forms them: scale, then the fp32 mask additions).  Otherwise
 // the row maximum is taken over the raw dot products and scale * log2(e)
 // enters through the exponent's FMA.  Maxima are kept in base-2 units.
-template <typename T, int D, bool MASKED, int QT>
+// CAUSAL (without MASKED): a key past the query is excluded outright.  With
+// causal masking alone no row is fully masked (key 0 is never past a query),
+// so exp(score - 1e9 - max) underflows to exactly 0 and the exclusion is the
+// same as the reference's -1e9 addition.
+template <typename T, int D, bool MASKED, bool CAUSAL, int QT, int KT>
 __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   constexpr int kWgQ = attn_wg_queries(QT);
-  using B = KvBlock<D>;
+  using B = KvBlock<D, KT>;
+  constexpr int kAttnKeys = B::kKeys;
   constexpr int KS = D / 32;                 // k-steps of the S^T product
   constexpr int DT = D / 16;                 // 16-row tiles of O^T
   constexpr int NL = 2 * B::kLoadsPerWave;   // loads per wave per block
@@ -140,7 +146,9 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   const int total = a.BH * a.qblocks;
   int lin = blockIdx.x;
   if ((total & 7) == 0) lin = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int bh = lin / a.qblocks, qb = lin - bh * a.qblocks;
+  const int bh = lin / a.qblocks;
+  int qb = lin - bh * a.qblocks;
+  if (CAUSAL) qb = a.qblocks - 1 - qb;       // the longest query blocks start first
   const int b = bh / a.H;
   const int64_t qhead = (int64_t)bh * a.M, khead = (int64_t)bh * a.N;
 
@@ -158,6 +166,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   __builtin_amdgcn_s_waitcnt(0x3f70);        // vmcnt(0): Q in registers before the loads below
   asm volatile("" ::: "memory");
 
+  const int qmin = qb * kWgQ + wave * 16 * QT;    // this wave's first query
   int nkb = (a.N + kAttnKeys - 1) / kAttnKeys;
   if (a.causal && a.mask_kind == GEV2_MASK_NONE) {
     // blocks whose every key is past every query here add exp(-1e9 + ...) = 0
@@ -181,11 +190,11 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
   // base-2 units throughout: x2 = score * log2(e), m in the same units
   const float xscale = a.scale * kLog2e;
 
-  load_kv<D>(rK, rV, khead, 0, a.N, wave, lane, k_lds(0), v_lds(0));
+  load_kv<D, KT>(rK, rV, khead, 0, a.N, wave, lane, k_lds(0), v_lds(0));
   for (int kb = 0; kb < nkb; ++kb) {
     const int st = kb & 1;
     if (kb + 1 < nkb) {
-      load_kv<D>(rK, rV, khead, (kb + 1) * kAttnKeys, a.N, wave, lane, k_lds(st ^ 1), v_lds(st ^ 1));
+      load_kv<D, KT>(rK, rV, khead, (kb + 1) * kAttnKeys, a.N, wave, lane, k_lds(st ^ 1), v_lds(st ^ 1));
       __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));   // this block's loads done
     } else {
       __builtin_amdgcn_s_waitcnt(0x3f70);
@@ -197,9 +206,9 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
     const bool tail = (kb + 1) * kAttnKeys > a.N;
 
     // S^T tiles: s[qt][kt] rows = keys 16 kt + 4 g + r, column = query q[qt]
-    f32x4_t s[QT][4];
+    f32x4_t s[QT][KT];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
       const int row = 16 * kt + col;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -213,17 +222,17 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
     }
 
     // online softmax; P^T packed as the B operand of O^T += V^T P^T
-    u32x4 pf[QT][2];
+    u32x4 pf[QT][KT / 2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       // x = the score in base-2 units: MASKED forms it as the reference does
       // (scale, then the fp32 mask additions); otherwise the scale (> 0) is
       // applied inside the exponent's FMA and the maximum taken over raw dots
-      float x[4][4];
+      float x[KT][4];
       float mloc = -INFINITY;
       const int key0 = kb * kAttnKeys + 4 * g;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float v = s[qt][kt][r];
@@ -234,16 +243,17 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
           x[kt][r] = v;
         }
       }
-      if (!MASKED && tail) {
-        // past the last key (zero-filled rows): out of the softmax
+      if (!MASKED && (tail || (CAUSAL && kb * kAttnKeys + kAttnKeys - 1 > qmin))) {
+        // past the last key (zero-filled rows), or past the query: out of the softmax
+        const int lim = CAUSAL ? min(a.N - 1, q[qt]) : a.N - 1;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
+        for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) x[kt][r] = key0 + 16 * kt + r < a.N ? x[kt][r] : -INFINITY;
+          for (int r = 0; r < 4; ++r) x[kt][r] = key0 + 16 * kt + r <= lim ? x[kt][r] : -INFINITY;
         }
       }
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) mloc = fmaxf(mloc, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
+      for (int kt = 0; kt < KT; ++kt) mloc = fmaxf(mloc, fmaxf(fmaxf(x[kt][0], x[kt][1]), fmaxf(x[kt][2], x[kt][3])));
       mloc = xor_max(xor_max(mloc, 16), 32);
       if constexpr (!MASKED) mloc *= xscale;
       const float m_new = fmaxf(m_run[qt], mloc);
@@ -252,9 +262,9 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
       const bool grew = m_new > m_run[qt];
       m_run[qt] = m_new;
       float lsum = 0.f;
-      uint32_t pb[4][4];
+      uint32_t pb[KT][4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float arg = MASKED ? x[kt][r] - m_new : fmaf(x[kt][r], xscale, -m_new);
@@ -272,7 +282,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
         }
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < KT / 2; ++j) {
         pf[qt][j][0] = pack2(pb[2 * j][0], pb[2 * j][1]);
         pf[qt][j][1] = pack2(pb[2 * j][2], pb[2 * j][3]);
         pf[qt][j][2] = pack2(pb[2 * j + 1][0], pb[2 * j + 1][1]);
@@ -284,7 +294,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
     // addresses key 32j + 16h + 4g + e, columns 16 dt + 4 cq ..
     const int e = (lane >> 2) & 3, cq = lane & 3;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < KT / 2; ++j) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         u32x4 vf;
@@ -325,12 +335,18 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
 
 template <typename T, int D, int QT>
 hipError_t launch_attn_fwd_qt(AttnArgs a, hipStream_t s) {
+  constexpr int KT = D == 64 ? 8 : 4;       // 128 keys per block at D = 64 (two workgroups per CU fit in LDS)
   a.qblocks = (a.M + attn_wg_queries(QT) - 1) / attn_wg_queries(QT);
   const int64_t blocks = (int64_t)a.BH * a.qblocks;
-  if (a.causal || a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f))
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true, QT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  if (a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f))
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true, false, QT, KT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       s, a);
+  else if (a.causal)
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false, true, QT, KT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       s, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false, QT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false, false, QT, KT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       s, a);
   return hipGetLastError();
 }
 
