@@ -419,6 +419,35 @@ __global__ void __launch_bounds__(256) attn_softmax_bwd_rows_kernel(const float*
   }
 }
 
+// 16-bit <-> fp32 copies for the backward of 16-bit tensors
+template <typename T>
+__global__ void __launch_bounds__(256) attn_widen_kernel(const T* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = Elem<T>::load1(src + i);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_narrow_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) Elem<T>::store1(dst + i, src[i]);
+}
+
+inline hipError_t convert(int dtype, bool widen, const void* src, void* dst, int64_t n, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+  if (dtype == GEV2_BF16) {
+    if (widen) hipLaunchKernelGGL(attn_widen_kernel<__bf16>, grid, dim3(256), 0, s, static_cast<const __bf16*>(src),
+                                  static_cast<float*>(dst), n);
+    else hipLaunchKernelGGL(attn_narrow_kernel<__bf16>, grid, dim3(256), 0, s, static_cast<const float*>(src),
+                            static_cast<__bf16*>(dst), n);
+  } else {
+    if (widen) hipLaunchKernelGGL(attn_widen_kernel<_Float16>, grid, dim3(256), 0, s,
+                                  static_cast<const _Float16*>(src), static_cast<float*>(dst), n);
+    else hipLaunchKernelGGL(attn_narrow_kernel<_Float16>, grid, dim3(256), 0, s, static_cast<const float*>(src),
+                            static_cast<_Float16*>(dst), n);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace gev2
 
 namespace {
@@ -490,11 +519,18 @@ extern "C" {
 
 const char* gev2_sdpa_last_error(void) { return t_attn_error.c_str(); }
 
+// fp32 copies of Q, K, V, dY and of dQ, dK, dV for a 16-bit backward
+int64_t widened_bytes(int64_t BH, int64_t M, int64_t N, int64_t D) {
+  return ((BH * (4 * M + 3 * N) * D * 4 + 255) / 256) * 256;
+}
+
 int64_t gev2_sdpa_workspace_size(const gev2_sdpa_desc* d, int backward) {
   gev2::AttnArgs a{};
   if (attn_check(d, &a) != GEV2_OK) return -1;
   if (fused_ok(d->dtype, d->D) && !backward) return 0;
-  return (backward ? 2 : 1) * scores_bytes(a.BH, d->M, d->N);
+  if (!backward) return scores_bytes(a.BH, d->M, d->N);
+  const int64_t wide = d->dtype == GEV2_F32 ? 0 : widened_bytes(a.BH, d->M, d->N, d->D);
+  return 2 * scores_bytes(a.BH, d->M, d->N) + wide;
 }
 
 int gev2_sdpa_fwd(const gev2_sdpa_desc* d, void* stream) {
@@ -538,14 +574,43 @@ int gev2_sdpa_bwd(const gev2_sdpa_bwd_desc* d, void* stream) {
   if (st != GEV2_OK) return st;
   if (!d->Q || !d->K || !d->V || !d->dY) return attn_fail(GEV2_MISSING_INPUT, "Q / K / V / dY is null");
   if (!d->dQ && !d->dK && !d->dV) return attn_fail(GEV2_INVALID, "all outputs null");   // launcher.cu:342
-  if (d->dtype != GEV2_F32) return attn_fail(GEV2_UNIMPLEMENTED, "16-bit attention backward is not implemented");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t M = d->M, N = d->N, D = d->D, BH = a.BH;
   const int64_t sb = scores_bytes(BH, M, N);
-  if (!d->workspace || d->workspace_bytes < 2 * sb)
+  const bool wide = d->dtype != GEV2_F32;
+  if (!d->workspace || d->workspace_bytes < 2 * sb + (wide ? widened_bytes(BH, M, N, D) : 0))
     return attn_fail(GEV2_MISSING_INPUT, "backward needs a workspace of gev2_sdpa_workspace_size(desc, 1) bytes");
   float* P = static_cast<float*>(d->workspace);
   float* dP = reinterpret_cast<float*>(static_cast<char*>(d->workspace) + sb);
+  if (wide) {
+    // 16-bit tensors: the fp32 path below on widened copies, gradients rounded back
+    float* w = reinterpret_cast<float*>(static_cast<char*>(d->workspace) + 2 * sb);
+    float *q = w, *k = q + BH * M * D, *v = k + BH * N * D, *dy = v + BH * N * D;
+    float *dq = dy + BH * M * D, *dk = dq + BH * M * D, *dv = dk + BH * N * D;
+    const void* src[4] = {d->Q, d->K, d->V, d->dY};
+    float* dst[4] = {q, k, v, dy};
+    const int64_t cnt[4] = {BH * M * D, BH * N * D, BH * N * D, BH * M * D};
+    for (int i = 0; i < 4; ++i) {
+      st = hip_status(gev2::convert(d->dtype, true, src[i], dst[i], cnt[i], s), "widen");
+      if (st != GEV2_OK) return st;
+    }
+    gev2_sdpa_bwd_desc f = *d;
+    f.dtype = GEV2_F32;
+    f.Q = q; f.K = k; f.V = v; f.dY = dy;
+    f.dQ = d->dQ ? dq : nullptr; f.dK = d->dK ? dk : nullptr; f.dV = d->dV ? dv : nullptr;
+    f.workspace_bytes = 2 * sb;
+    st = gev2_sdpa_bwd(&f, stream);
+    if (st != GEV2_OK) return st;
+    void* outs[3] = {d->dQ, d->dK, d->dV};
+    const float* res[3] = {dq, dk, dv};
+    const int64_t on[3] = {BH * M * D, BH * N * D, BH * N * D};
+    for (int i = 0; i < 3; ++i) {
+      if (!outs[i]) continue;
+      st = hip_status(gev2::convert(d->dtype, false, res[i], outs[i], on[i], s), "narrow");
+      if (st != GEV2_OK) return st;
+    }
+    return GEV2_OK;
+  }
   // P = softmax(scale Q K^T + masks)
   st = slice_gemm(GEV2_F32, false, true, a.scale, BH, M, N, D, d->Q, D, M * D, d->K, D, N * D, P, N, M * N, stream);
   if (st != GEV2_OK) return st;

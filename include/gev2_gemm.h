@@ -290,9 +290,12 @@ const char* gev2_rnn_last_error(void);
  * scale 0 means 1/sqrt(D).  causal adds -1e9 where key > query; mask
  * [B,1,M,N] (broadcast over H): I8 / I32 entries != 0 add -1e9, F32 entries
  * are added.  dropout_p must be 0 (GEV2_UNIMPLEMENTED otherwise).
- * F16 / BF16 with D = 64 or 128: one fused kernel, no workspace; `lse`
- * (optional, fp32 [B,H,M]) receives each row's log-sum-exp.
- * F32: S / P in `workspace` (gev2_sdpa_workspace_size bytes).
+ * Forward, F16 / BF16 with D = 64 or 128: one fused kernel, no workspace;
+ * `lse` (optional, fp32 [B,H,M]) receives each row's log-sum-exp.
+ * Forward, F32: S / P in `workspace` (gev2_sdpa_workspace_size bytes).
+ * Backward: the reference's algorithm batched over all (b, h) slices in fp32,
+ * with P and dP in `workspace`; 16-bit tensors are widened to fp32 copies in
+ * the same workspace and the gradients rounded back.
  */
 enum { GEV2_MASK_NONE = 0, GEV2_MASK_I8 = 1, GEV2_MASK_I32 = 2, GEV2_MASK_F32 = 3 };
 

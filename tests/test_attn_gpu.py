@@ -139,3 +139,34 @@ def test_validation(capi):
     assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 10           # mask kind without a mask
     b = capi.SdpaBwdDesc(dtype=F32, B=1, H=1, M=8, N=8, D=16, Q=16, K=32, V=48, dY=64)
     assert L.gev2_sdpa_bwd(ctypes.byref(b), None) == 1            # all outputs null (launcher.cu:342)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("causal,mk", [(False, O.MASK_NONE), (True, O.MASK_I32)], ids=["plain", "causal-i32"])
+def test_16bit_backward(capi, dtype, causal, mk):
+    """16-bit tensors: fp32 arithmetic on the exact 16-bit inputs, each gradient rounded once
+    to the storage type: |g - g64| <= eps |g64| + 1e-5 max|g64|."""
+    B, H, M, N, D = 1, 2, 40, 56, 64
+    Q, K, V = _qkv(27, B, H, M, N, D, dtype)
+    dY = rounded(np.random.default_rng(28).standard_normal(Q.shape), dtype).astype(np.float32)
+    mask = _mask(mk, B, M, N, 29)
+    bufs = [capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype)) for a in (Q, K, V, dY)]
+    es = capi.elem_bytes(dtype)
+    outs = [capi.DeviceBuffer(a.size * es) for a in (Q, K, V)]
+    mkb = capi.DeviceBuffer.from_numpy(mask) if mask is not None else None
+    L = capi.lib()
+    fd = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D)
+    wsb = L.gev2_sdpa_workspace_size(ctypes.byref(fd), 1)
+    ws = capi.DeviceBuffer(wsb)
+    d = capi.SdpaBwdDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal), mask_kind=mk,
+                         mask=mkb.ptr if mkb else None, Q=bufs[0].ptr, K=bufs[1].ptr, V=bufs[2].ptr, dY=bufs[3].ptr,
+                         dQ=outs[0].ptr, dK=outs[1].ptr, dV=outs[2].ptr, workspace=ws.ptr, workspace_bytes=wsb)
+    capi.check_sdpa(L.gev2_sdpa_bwd(ctypes.byref(d), None), "sdpa bwd 16-bit")
+    capi.synchronize()
+    ref = O.sdpa_backward(Q, K, V, dY, causal=causal, mask=mask, mask_kind=mk)
+    st = capi.to_storage(np.zeros(1, np.float32), dtype).dtype
+    eps = O.storage_eps(dtype)
+    for name, buf, a in zip(("dQ", "dK", "dV"), outs, (Q, K, V)):
+        g = capi.from_storage(buf.download(a.shape, st), dtype)
+        r = ref[name]
+        assert np.all(np.abs(g - r) <= eps * np.abs(r) + 1e-5 * np.abs(r).max()), name
