@@ -610,4 +610,35 @@ int gev2_event_elapsed_ms(float* ms, void* start, void* stop) {
   return GEV2_OK;
 }
 
+// HIP graph capture of a stream's work (thread-local capture mode: other
+// threads' HIP calls are unaffected).  Capture is valid only for work that
+// allocates nothing: pass every workspace, or make one call outside the
+// capture first so that the per-stream buffer already exists.
+int gev2_graph_begin(void* stream) {
+  if (!stream) return fail(GEV2_INVALID_ARGUMENT, "capture needs a created stream, not the null stream");
+  GEV2_HIP_CALL(hipStreamBeginCapture(reinterpret_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
+                "hipStreamBeginCapture");
+  return GEV2_OK;
+}
+int gev2_graph_end(void* stream, void** exec) {
+  if (!exec) return fail(GEV2_INVALID_ARGUMENT, "exec is null");
+  hipGraph_t g = nullptr;
+  GEV2_HIP_CALL(hipStreamEndCapture(reinterpret_cast<hipStream_t>(stream), &g), "hipStreamEndCapture");
+  hipGraphExec_t e = nullptr;
+  const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (err != hipSuccess) return hip_fail(err, "hipGraphInstantiate");
+  *exec = e;
+  return GEV2_OK;
+}
+int gev2_graph_launch(void* exec, void* stream) {
+  GEV2_HIP_CALL(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), reinterpret_cast<hipStream_t>(stream)),
+                "hipGraphLaunch");
+  return GEV2_OK;
+}
+int gev2_graph_destroy(void* exec) {
+  GEV2_HIP_CALL(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)), "hipGraphExecDestroy");
+  return GEV2_OK;
+}
+
 }  // extern "C"

@@ -30,6 +30,7 @@ EXPORTED = [
     "gev2_conv2d_fwd", "gev2_conv2d_bwd", "gev2_conv2d_last_error",
     "gev2_rnn_fwd", "gev2_rnn_bwd", "gev2_rnn_last_error",
     "gev2_sdpa_fwd", "gev2_sdpa_bwd", "gev2_sdpa_workspace_size", "gev2_sdpa_last_error",
+    "gev2_graph_begin", "gev2_graph_end", "gev2_graph_launch", "gev2_graph_destroy",
 ]
 
 
@@ -199,6 +200,10 @@ def lib() -> ctypes.CDLL:
     L.gev2_rnn_bwd.argtypes = [ctypes.POINTER(RnnBwdDesc), vp]
     L.gev2_rnn_last_error.restype = ctypes.c_char_p
     L.gev2_rnn_last_error.argtypes = []
+    L.gev2_graph_begin.argtypes = [vp]
+    L.gev2_graph_end.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p)]
+    L.gev2_graph_launch.argtypes = [vp, vp]
+    L.gev2_graph_destroy.argtypes = [vp]
     L.gev2_sdpa_fwd.argtypes = [ctypes.POINTER(SdpaDesc), vp]
     L.gev2_sdpa_bwd.argtypes = [ctypes.POINTER(SdpaBwdDesc), vp]
     L.gev2_sdpa_workspace_size.restype = ctypes.c_int64

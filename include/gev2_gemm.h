@@ -396,6 +396,19 @@ int gev2_event_record(void* event, void* stream);
 int gev2_event_synchronize(void* event);
 int gev2_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/*
+ * HIP graph capture of a stream's work: begin, run the calls to record on
+ * `stream`, end (instantiates; *exec receives the executable graph), then
+ * launch it any number of times and destroy it.  Replaces the CuPy graph
+ * capture of the reference's Python layer (graph/graph_exec.py:119-136).  Only
+ * work that allocates nothing may be captured: pass every workspace, or make
+ * one call outside the capture first (the per-stream buffer then exists).
+ */
+int gev2_graph_begin(void* stream);
+int gev2_graph_end(void* stream, void** exec);
+int gev2_graph_launch(void* exec, void* stream);
+int gev2_graph_destroy(void* exec);
+
 #ifdef __cplusplus
 }
 #endif
