@@ -419,6 +419,372 @@ __global__ void __launch_bounds__(256) attn_softmax_bwd_rows_kernel(const float*
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused backward of the 16-bit forward (flash style): P is recomputed from the
+// forward's row log-sum-exp, never stored.
+//   attn_bwd_dot_kernel:  Dq[q] = sum_d dO[q][d] O[q][d]
+//   attn_bwd_kv_kernel:   a workgroup owns 64 keys (16 per wave, K / V rows in
+//     registers) and streams 64-query blocks of Q and dO through LDS:
+//     S = Q K^T and dP = dO V^T come out with the key in the lane, so
+//     P = exp(scale S - lse) and dS = P (dP - Dq) feed dV^T += dO^T P and
+//     dK^T += Q^T dS as B operands straight from registers (dO and Q read with
+//     transpose reads, queries in the matching permuted order).
+//   attn_bwd_q_kernel:    the forward's layout (query in the lane, 16 per
+//     wave): S^T = K Q^T, dP^T = V dO^T, dS^T, dQ^T += K^T dS^T.
+// Masked entries get dS = 0, as the reference zeroes them (any non-zero
+// external mask entry, or key > query with causal).
+// ---------------------------------------------------------------------------
+struct AttnBwdArgs {
+  AttnArgs f;            // Q, K, V, scale, masks, dims (f.Y = O, f.lse = lse)
+  const void* dO;
+  const float* Dq;       // [BH, M]
+  void* dQ;
+  void* dK;
+  void* dV;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_dot_kernel(const T* __restrict__ dO, const T* __restrict__ O,
+                                                           float* __restrict__ Dq, int64_t rows, int D) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float acc = 0.f;
+  for (int d = lane; d < D; d += 64) acc += Elem<T>::load1(dO + row * D + d) * Elem<T>::load1(O + row * D + d);
+  for (int o = 32; o > 0; o >>= 1) acc = xor_sum(acc, o);
+  if (lane == 0) Dq[row] = acc;
+}
+
+// 16-byte row piece (8 elements from 8 * chunk) of a tile whose rows hold
+// 32-byte blocks XOR-swizzled by (row & 3)
+__device__ __forceinline__ u32x4 row16_b32swz(const char* base, int row_bytes, int row, int chunk) {
+  return *reinterpret_cast<const u32x4*>(base + row * row_bytes + ((((chunk >> 1) ^ (row & 3))) << 5) +
+                                         ((chunk & 1) << 4));
+}
+
+// Transpose-read operand: lane 16g + i receives rows {r0 + 4g + e, r0 + 16 + 4g + e}
+// (e = 0..3) of column 16 dt + i from a tile with 32-byte blocks swizzled by (row & 3).
+__device__ __forceinline__ u32x4 tr_operand(const char* base, int row_bytes, int r0, int dt, int lane) {
+  const int g = lane >> 4, e = (lane >> 2) & 3, cq = lane & 3;
+  u32x4 f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = r0 + 16 * h + 4 * g + e;
+    const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(base + row * row_bytes + ((dt ^ (row & 3)) << 5) + cq * 8));
+    const u32x2 w2 = __builtin_bit_cast(u32x2, v);
+    f[2 * h] = w2[0];
+    f[2 * h + 1] = w2[1];
+  }
+  return f;
+}
+
+// Whether (query q, key) is masked for the dS zeroing (and the score).
+__device__ __forceinline__ bool masked_entry(const AttnArgs& a, int b, int q, int key) {
+  bool m = a.causal && key > q;
+  if (a.mask_kind != GEV2_MASK_NONE) {
+    const int64_t i = ((int64_t)b * a.M + q) * a.N + key;
+    if (a.mask_kind == GEV2_MASK_I8) m |= static_cast<const int8_t*>(a.mask)[i] != 0;
+    else if (a.mask_kind == GEV2_MASK_I32) m |= static_cast<const int32_t*>(a.mask)[i] != 0;
+    else m |= static_cast<const float*>(a.mask)[i] != 0.f;
+  }
+  return m;
+}
+
+// DMA one 64-row tile of a [rows, D] tensor (rows past `limit` read as zero)
+// into LDS with 32-byte blocks swizzled by (row & 3); this wave's share.
+template <int D>
+__device__ __forceinline__ void load_rows_b32swz(const i32x4_t& r, int64_t head_off, int row0, int limit, int wave,
+                                                 int lane, uint32_t lds) {
+  constexpr int kRowBytes = D * 2, kChunks = D / 8, rows_per_load = 1024 / kRowBytes;
+  constexpr int loads = 64 * kRowBytes / 1024 / 4;
+#pragma unroll
+  for (int j = 0; j < loads; ++j) {
+    const int ld = wave * loads + j;
+    const int row = ld * rows_per_load + lane / kChunks;
+    const int pc = lane % kChunks;
+    const int c = (((pc >> 1) ^ (row & 3)) << 1) | (pc & 1);
+    const int off = row0 + row < limit ? static_cast<int>(((head_off + row0 + row) * D + c * 8) * 2) : kOobOffset;
+    dma16(r, off, 0, lds + ld * 1024);
+  }
+}
+
+// Same with 16-byte chunks swizzled by (row & 7) (rows read whole only).
+template <int D>
+__device__ __forceinline__ void load_rows_c16swz(const i32x4_t& r, int64_t head_off, int row0, int limit, int wave,
+                                                 int lane, uint32_t lds) {
+  constexpr int kRowBytes = D * 2, kChunks = D / 8, rows_per_load = 1024 / kRowBytes;
+  constexpr int loads = 64 * kRowBytes / 1024 / 4;
+#pragma unroll
+  for (int j = 0; j < loads; ++j) {
+    const int ld = wave * loads + j;
+    const int row = ld * rows_per_load + lane / kChunks;
+    const int pc = lane % kChunks;
+    const int c = pc ^ (row & 7);
+    const int off = row0 + row < limit ? static_cast<int>(((head_off + row0 + row) * D + c * 8) * 2) : kOobOffset;
+    dma16(r, off, 0, lds + ld * 1024);
+  }
+}
+
+template <typename T, int D, bool MASKED>
+__global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
+  const AttnArgs& a = ba.f;
+  constexpr int KS = D / 32, DT = D / 16, RB = D * 2, TILE = 64 * RB;
+  constexpr int NL = 2 * (TILE / 1024 / 4);          // loads per wave per query block (Q and dO)
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int kblocks = (a.N + 63) / 64;
+  const int bh = blockIdx.x / kblocks, kb = blockIdx.x - bh * kblocks;
+  const int b = bh / a.H;
+  const int64_t qhead = (int64_t)bh * a.M, khead = (int64_t)bh * a.N;
+  const int key = kb * 64 + wave * 16 + col;          // this lane's key column
+  const bool key_ok = key < a.N;
+
+  // K and V rows of this lane's key as B operands (k = d 32 ks + 8 g ..)
+  u32x4 kf[KS], vf[KS];
+  {
+    const T* krow = static_cast<const T*>(a.K) + (khead + key) * D;
+    const T* vrow = static_cast<const T*>(a.V) + (khead + key) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[ks] = key_ok ? *reinterpret_cast<const u32x4*>(krow + 32 * ks + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      vf[ks] = key_ok ? *reinterpret_cast<const u32x4*>(vrow + 32 * ks + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x3f70);
+  asm volatile("" ::: "memory");
+
+  const float kLog2e = 1.4426950408889634f;
+  const float xscale = a.scale * kLog2e;
+  f32x4_t dk[DT], dv[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dk[dt] = dv[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nqb = (a.M + 63) / 64;
+  // causal without other masks: query blocks wholly before this block's first key see none of it
+  const int qb0 = (!MASKED && a.causal) ? min(nqb, (kb * 64) / 64) : 0;
+  const i32x4_t rQ = rsrc_words(a.Q), rO = rsrc_words(ba.dO);
+  const uint32_t base = lds_addr(&lds[0][0][0]);
+  auto q_lds = [&](int st) { return base + st * 2 * TILE; };
+  auto o_lds = [&](int st) { return base + st * 2 * TILE + TILE; };
+  if (qb0 < nqb) {
+    load_rows_b32swz<D>(rQ, qhead, qb0 * 64, a.M, wave, lane, q_lds(0));
+    load_rows_b32swz<D>(rO, qhead, qb0 * 64, a.M, wave, lane, o_lds(0));
+  }
+  for (int qb = qb0; qb < nqb; ++qb) {
+    const int st = (qb - qb0) & 1;
+    if (qb + 1 < nqb) {
+      load_rows_b32swz<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
+      load_rows_b32swz<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
+      __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x3f70);
+    }
+    __syncthreads();
+    asm volatile("" ::: "memory");
+    const char* ql = &lds[st][0][0];
+    const char* ol = &lds[st][1][0];
+    uint32_t pw[4][2], sw[4][2];                      // P and dS of each 16-query tile, packed pairs
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f32x4_t sacc = f32x4_t{0.f, 0.f, 0.f, 0.f}, pacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = mfma_16x16x32<T>(row16_b32swz(ql, RB, 16 * t + col, 4 * ks + g), kf[ks], sacc);
+        pacc = mfma_16x16x32<T>(row16_b32swz(ol, RB, 16 * t + col, 4 * ks + g), vf[ks], pacc);
+      }
+      float p[4], ds[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = qb * 64 + 16 * t + 4 * g + r;   // row of this accumulator entry
+        const bool q_ok = q < a.M;
+        const float lse2 = q_ok ? a.lse[qhead + q] * kLog2e : INFINITY;
+        const float dq = q_ok ? ba.Dq[qhead + q] : 0.f;
+        float pv;
+        if constexpr (MASKED) {
+          const float x = (key_ok && q_ok) ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : -INFINITY;
+          pv = __builtin_amdgcn_exp2f(x - lse2);
+          const bool m = (key_ok && q_ok) ? masked_entry(a, b, q, key) : true;
+          ds[r] = m ? 0.f : pv * (pacc[r] - dq);
+        } else {
+          const bool live = key_ok && q_ok && !(a.causal && key > q);
+          pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
+          ds[r] = pv * (pacc[r] - dq);
+        }
+        p[r] = pv;
+      }
+      pw[t][0] = pack2(Elem<T>::bits(p[0]), Elem<T>::bits(p[1]));
+      pw[t][1] = pack2(Elem<T>::bits(p[2]), Elem<T>::bits(p[3]));
+      sw[t][0] = pack2(Elem<T>::bits(ds[0]), Elem<T>::bits(ds[1]));
+      sw[t][1] = pack2(Elem<T>::bits(ds[2]), Elem<T>::bits(ds[3]));
+    }
+    // dV^T[d][key] += dO^T P ; dK^T[d][key] += Q^T dS  (queries 32 i + {4g + e, 16 + 4g + e})
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 pb = {pw[2 * i][0], pw[2 * i][1], pw[2 * i + 1][0], pw[2 * i + 1][1]};
+      const u32x4 sb = {sw[2 * i][0], sw[2 * i][1], sw[2 * i + 1][0], sw[2 * i + 1][1]};
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dv[dt] = mfma_16x16x32<T>(tr_operand(ol, RB, 32 * i, dt, lane), pb, dv[dt]);
+        dk[dt] = mfma_16x16x32<T>(tr_operand(ql, RB, 32 * i, dt, lane), sb, dk[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  if (!key_ok) return;
+  T* dkr = static_cast<T*>(ba.dK) + (khead + key) * D;
+  T* dvr = static_cast<T*>(ba.dV) + (khead + key) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    if (ba.dK) {
+      u32x2 w;
+      w[0] = pack2(Elem<T>::bits(dk[dt][0] * a.scale), Elem<T>::bits(dk[dt][1] * a.scale));
+      w[1] = pack2(Elem<T>::bits(dk[dt][2] * a.scale), Elem<T>::bits(dk[dt][3] * a.scale));
+      *reinterpret_cast<u32x2*>(dkr + 16 * dt + 4 * g) = w;
+    }
+    if (ba.dV) {
+      u32x2 w;
+      w[0] = pack2(Elem<T>::bits(dv[dt][0]), Elem<T>::bits(dv[dt][1]));
+      w[1] = pack2(Elem<T>::bits(dv[dt][2]), Elem<T>::bits(dv[dt][3]));
+      *reinterpret_cast<u32x2*>(dvr + 16 * dt + 4 * g) = w;
+    }
+  }
+}
+
+template <typename T, int D, bool MASKED>
+__global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnBwdArgs ba) {
+  const AttnArgs& a = ba.f;
+  constexpr int KS = D / 32, DT = D / 16, RB = D * 2, TILE = 64 * RB;
+  constexpr int NL = 2 * (TILE / 1024 / 4);
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int qblocks = (a.M + 63) / 64;
+  const int bh = blockIdx.x / qblocks, qb = blockIdx.x - bh * qblocks;
+  const int b = bh / a.H;
+  const int64_t qhead = (int64_t)bh * a.M, khead = (int64_t)bh * a.N;
+  const int q = qb * 64 + wave * 16 + col;            // this lane's query column
+  const bool q_ok = q < a.M;
+
+  u32x4 qf[KS], of[KS];
+  {
+    const T* qrow = static_cast<const T*>(a.Q) + (qhead + q) * D;
+    const T* orow = static_cast<const T*>(ba.dO) + (qhead + q) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = q_ok ? *reinterpret_cast<const u32x4*>(qrow + 32 * ks + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      of[ks] = q_ok ? *reinterpret_cast<const u32x4*>(orow + 32 * ks + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const float kLog2e = 1.4426950408889634f;
+  const float xscale = a.scale * kLog2e;
+  const float lse2 = q_ok ? a.lse[qhead + q] * kLog2e : INFINITY;
+  const float dq = q_ok ? ba.Dq[qhead + q] : 0.f;
+  __builtin_amdgcn_s_waitcnt(0x3f70);
+  asm volatile("" ::: "memory");
+
+  f32x4_t acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int nkb = (a.N + 63) / 64;
+  if (!MASKED && a.causal) nkb = min(nkb, (qb * 64 + 63) / 64 + 1);
+  const i32x4_t rK = rsrc_words(a.K), rV = rsrc_words(a.V);
+  const uint32_t base = lds_addr(&lds[0][0][0]);
+  auto k_lds = [&](int st) { return base + st * 2 * TILE; };
+  auto v_lds = [&](int st) { return base + st * 2 * TILE + TILE; };
+  load_rows_b32swz<D>(rK, khead, 0, a.N, wave, lane, k_lds(0));
+  load_rows_c16swz<D>(rV, khead, 0, a.N, wave, lane, v_lds(0));
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int st = kb & 1;
+    if (kb + 1 < nkb) {
+      load_rows_b32swz<D>(rK, khead, (kb + 1) * 64, a.N, wave, lane, k_lds(st ^ 1));
+      load_rows_c16swz<D>(rV, khead, (kb + 1) * 64, a.N, wave, lane, v_lds(st ^ 1));
+      __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x3f70);
+    }
+    __syncthreads();
+    asm volatile("" ::: "memory");
+    const char* kl = &lds[st][0][0];
+    const char* vl = &lds[st][1][0];
+    uint32_t sw[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      f32x4_t sacc = f32x4_t{0.f, 0.f, 0.f, 0.f}, pacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const int row = 16 * kt + col;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = mfma_16x16x32<T>(row16_b32swz(kl, RB, row, 4 * ks + g), qf[ks], sacc);
+        const int c = (4 * ks + g) ^ (row & 7);
+        pacc = mfma_16x16x32<T>(*reinterpret_cast<const u32x4*>(vl + row * RB + c * 16), of[ks], pacc);
+      }
+      float ds[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb * 64 + 16 * kt + 4 * g + r;
+        const bool key_ok = key < a.N;
+        if constexpr (MASKED) {
+          const float x = (key_ok && q_ok) ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : -INFINITY;
+          const float pv = __builtin_amdgcn_exp2f(x - lse2);
+          const bool m = (key_ok && q_ok) ? masked_entry(a, b, q, key) : true;
+          ds[r] = m ? 0.f : pv * (pacc[r] - dq);
+        } else {
+          const bool live = key_ok && q_ok && !(a.causal && key > q);
+          const float pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
+          ds[r] = pv * (pacc[r] - dq);
+        }
+      }
+      sw[kt][0] = pack2(Elem<T>::bits(ds[0]), Elem<T>::bits(ds[1]));
+      sw[kt][1] = pack2(Elem<T>::bits(ds[2]), Elem<T>::bits(ds[3]));
+    }
+    // dQ^T[d][q] += K^T[d][key] dS^T[key][q]  (keys 32 j + {4g + e, 16 + 4g + e})
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 sb = {sw[2 * j][0], sw[2 * j][1], sw[2 * j + 1][0], sw[2 * j + 1][1]};
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma_16x16x32<T>(tr_operand(kl, RB, 32 * j, dt, lane), sb, acc[dt]);
+    }
+    __syncthreads();
+  }
+  if (!q_ok) return;
+  T* dqr = static_cast<T*>(ba.dQ) + (qhead + q) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    u32x2 w;
+    w[0] = pack2(Elem<T>::bits(acc[dt][0] * a.scale), Elem<T>::bits(acc[dt][1] * a.scale));
+    w[1] = pack2(Elem<T>::bits(acc[dt][2] * a.scale), Elem<T>::bits(acc[dt][3] * a.scale));
+    *reinterpret_cast<u32x2*>(dqr + 16 * dt + 4 * g) = w;
+  }
+}
+
+template <typename T, int D>
+hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
+  const AttnArgs& a = ba.f;
+  const int64_t rows = (int64_t)a.BH * a.M;
+  hipLaunchKernelGGL((attn_bwd_dot_kernel<T>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s,
+                     static_cast<const T*>(ba.dO), static_cast<const T*>(a.Y), const_cast<float*>(ba.Dq), rows, D);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const bool masked = a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f);
+  if (ba.dK || ba.dV) {
+    const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.N + 63) / 64)));
+    if (masked) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true>), grid, dim3(256), 0, s, ba);
+    else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false>), grid, dim3(256), 0, s, ba);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (ba.dQ) {
+    const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.M + 63) / 64)));
+    if (masked) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true>), grid, dim3(256), 0, s, ba);
+    else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false>), grid, dim3(256), 0, s, ba);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
 // 16-bit <-> fp32 copies for the backward of 16-bit tensors
 template <typename T>
 __global__ void __launch_bounds__(256) attn_widen_kernel(const T* __restrict__ src, float* __restrict__ dst, int64_t n) {
@@ -524,11 +890,26 @@ int64_t widened_bytes(int64_t BH, int64_t M, int64_t N, int64_t D) {
   return ((BH * (4 * M + 3 * N) * D * 4 + 255) / 256) * 256;
 }
 
+int64_t align256(int64_t n) { return ((n + 255) / 256) * 256; }
+
+// fused 16-bit backward: O [BH, M, D] (16-bit), lse and Dq [BH, M] fp32
+int64_t fused_bwd_bytes(int64_t BH, int64_t M, int64_t D) {
+  return align256(BH * M * D * 2) + 2 * align256(BH * M * 4);
+}
+
+// the fused backward unless GEV2_ATTN_BWD_WIDE=1 (comparison runs)
+bool fused_bwd(int dtype, int D) {
+  if (!fused_ok(dtype, D)) return false;
+  const char* v = std::getenv("GEV2_ATTN_BWD_WIDE");
+  return !(v && v[0] == '1');
+}
+
 int64_t gev2_sdpa_workspace_size(const gev2_sdpa_desc* d, int backward) {
   gev2::AttnArgs a{};
   if (attn_check(d, &a) != GEV2_OK) return -1;
   if (fused_ok(d->dtype, d->D) && !backward) return 0;
   if (!backward) return scores_bytes(a.BH, d->M, d->N);
+  if (fused_bwd(d->dtype, d->D)) return fused_bwd_bytes(a.BH, d->M, d->D);
   const int64_t wide = d->dtype == GEV2_F32 ? 0 : widened_bytes(a.BH, d->M, d->N, d->D);
   return 2 * scores_bytes(a.BH, d->M, d->N) + wide;
 }
@@ -576,6 +957,33 @@ int gev2_sdpa_bwd(const gev2_sdpa_bwd_desc* d, void* stream) {
   if (!d->dQ && !d->dK && !d->dV) return attn_fail(GEV2_INVALID, "all outputs null");   // launcher.cu:342
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t M = d->M, N = d->N, D = d->D, BH = a.BH;
+  if (fused_bwd(d->dtype, d->D)) {
+    // recompute O and lse with the fused forward, Dq = rowsum(dO O), then the dK/dV and dQ kernels
+    if (!d->workspace || d->workspace_bytes < fused_bwd_bytes(BH, M, D))
+      return attn_fail(GEV2_MISSING_INPUT, "backward needs a workspace of gev2_sdpa_workspace_size(desc, 1) bytes");
+    for (const void* p : {d->Q, d->K, d->V, d->dY, static_cast<const void*>(d->dQ), static_cast<const void*>(d->dK),
+                          static_cast<const void*>(d->dV)})
+      if (reinterpret_cast<uintptr_t>(p) % 16) return attn_fail(GEV2_INVALID, "fused path needs 16-byte aligned tensors");
+    if (BH * M * D * 2 > 0x7fffff00LL || BH * N * D * 2 > 0x7fffff00LL)
+      return attn_fail(GEV2_INVALID, "fused path needs Q / K / V / dY under 2^31 bytes");
+    char* w = static_cast<char*>(d->workspace);
+    void* O = w;
+    float* lse = reinterpret_cast<float*>(w + align256(BH * M * D * 2));
+    float* Dq = reinterpret_cast<float*>(w + align256(BH * M * D * 2) + align256(BH * M * 4));
+    gev2::AttnArgs fa = a;
+    fa.Q = d->Q; fa.K = d->K; fa.V = d->V; fa.Y = O; fa.lse = lse;
+    hipError_t e;
+    if (d->dtype == GEV2_BF16) e = D == 64 ? gev2::launch_attn_fwd<__bf16, 64>(fa, s) : gev2::launch_attn_fwd<__bf16, 128>(fa, s);
+    else e = D == 64 ? gev2::launch_attn_fwd<_Float16, 64>(fa, s) : gev2::launch_attn_fwd<_Float16, 128>(fa, s);
+    st = hip_status(e, "attn_fwd (backward)");
+    if (st != GEV2_OK) return st;
+    gev2::AttnBwdArgs ba{};
+    ba.f = fa;
+    ba.dO = d->dY; ba.Dq = Dq; ba.dQ = d->dQ; ba.dK = d->dK; ba.dV = d->dV;
+    if (d->dtype == GEV2_BF16) e = D == 64 ? gev2::launch_attn_bwd<__bf16, 64>(ba, s) : gev2::launch_attn_bwd<__bf16, 128>(ba, s);
+    else e = D == 64 ? gev2::launch_attn_bwd<_Float16, 64>(ba, s) : gev2::launch_attn_bwd<_Float16, 128>(ba, s);
+    return hip_status(e, "attn_bwd");
+  }
   const int64_t sb = scores_bytes(BH, M, N);
   const bool wide = d->dtype != GEV2_F32;
   if (!d->workspace || d->workspace_bytes < 2 * sb + (wide ? widened_bytes(BH, M, N, D) : 0))

@@ -362,6 +362,32 @@ def attn_cfg(ctx, dtype, iters, B=8, H=8, M=512, N=512, D=64, causal=False, sets
             "tflops": flop / (ms * 1e-3) / 1e12, "gbps_algorithmic": byt / (ms * 1e-3) / 1e9}
 
 
+def attn_bwd_cfg(ctx, dtype, iters, B=8, H=8, M=512, N=512, D=64, causal=False):
+    """C4 shape through gev2_sdpa_bwd (dQ, dK, dV): for 16-bit tensors the fused backward
+    (forward recomputed for O and lse, Dq, dK/dV kernel, dQ kernel); GEV2_ATTN_BWD_WIDE=1 selects
+    the batched fp32 path on widened copies."""
+    capi = ctx.capi
+    es = capi.elem_bytes(dtype)
+    g = np.random.default_rng(59)
+    L = capi.lib()
+    Q, K, V, dY = (capi.to_storage(normal(g, s), dtype) for s in ((B, H, M, D), (B, H, N, D), (B, H, N, D),
+                                                                    (B, H, M, D)))
+    fd = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal))
+    wsb = L.gev2_sdpa_workspace_size(ctypes.byref(fd), 1)
+    d = capi.SdpaBwdDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal), Q=ctx.put(Q), K=ctx.put(K),
+                         V=ctx.put(V), dY=ctx.put(dY), dQ=ctx.empty(B * H * M * D * es),
+                         dK=ctx.empty(B * H * N * D * es), dV=ctx.empty(B * H * N * D * es),
+                         workspace=ctx.empty(wsb), workspace_bytes=wsb)
+
+    def bwd():
+        capi.check_sdpa(L.gev2_sdpa_bwd(ctypes.byref(d), ctx.stream.ptr), "sdpa bwd")
+
+    ms = ctx.time_ms(bwd, iters)
+    flop = 10.0 * B * H * M * N * D * (0.5 if causal else 1.0)    # incl. the recomputed forward
+    return {"shape": f"B={B} H={H} M={M} N={N} D={D}" + (" causal" if causal else ""), "bwd_us": ms * 1e3,
+            "tflops": flop / (ms * 1e-3) / 1e12, "workspace_bytes": wsb}
+
+
 def skinny_cfg(ctx, iters, sets=10):
     """C5b: bf16 M=8, N=K=4096 + bias; 10 distinct W (335 MB) rotate past the MALL.
     The split-K partials go to a caller workspace (gev2_gemm_fwd_workspace_size)."""
@@ -481,6 +507,8 @@ def main():
             ("c4_attn_fused_bf16", lambda: attn_cfg(ctx, capi.BF16, 50)),
             ("c4_attn_fused_bf16_causal", lambda: attn_cfg(ctx, capi.BF16, 50, causal=True)),
             ("c4_attn_f32", lambda: attn_cfg(ctx, capi.F32, 10, sets=2)),
+            ("c4_attn_bwd_bf16", lambda: attn_bwd_cfg(ctx, capi.BF16, 20)),
+            ("c4_attn_bwd_bf16_causal", lambda: attn_bwd_cfg(ctx, capi.BF16, 20, causal=True)),
             ("c5a_conv_f32", lambda: conv_cfg(ctx, capi.F32, 20)),
             ("c5a_conv_bf16", lambda: conv_cfg(ctx, capi.BF16, 20)),
             ("c5a_conv2d_op_f32_per_image", lambda: conv_op_cfg(ctx, capi.F32, 5, 1)),

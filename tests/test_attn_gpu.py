@@ -141,12 +141,30 @@ def test_validation(capi):
     assert L.gev2_sdpa_bwd(ctypes.byref(b), None) == 1            # all outputs null (launcher.cu:342)
 
 
+BWD_CASES = [
+    # (B, H, M, N, D, causal, mask kind)
+    (1, 2, 40, 56, 64, False, O.MASK_NONE),
+    (1, 2, 40, 56, 64, True, O.MASK_I32),
+    (2, 1, 130, 70, 64, False, O.MASK_NONE),
+    (1, 2, 96, 128, 128, True, O.MASK_NONE),
+    (1, 1, 72, 100, 128, False, O.MASK_I8),
+    (1, 2, 64, 80, 64, False, O.MASK_F32),
+]
+
+
+@pytest.mark.parametrize("path", ["fused", "wide"])
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
-@pytest.mark.parametrize("causal,mk", [(False, O.MASK_NONE), (True, O.MASK_I32)], ids=["plain", "causal-i32"])
-def test_16bit_backward(capi, dtype, causal, mk):
-    """16-bit tensors: fp32 arithmetic on the exact 16-bit inputs, each gradient rounded once
-    to the storage type: |g - g64| <= eps |g64| + 1e-5 max|g64|."""
-    B, H, M, N, D = 1, 2, 40, 56, 64
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: "B{}H{}M{}N{}D{}{}{}".format(
+    *c[:5], "-causal" if c[5] else "", ["", "-i8", "-i32", "-f32"][c[6]]))
+def test_16bit_backward(capi, dtype, case, path, monkeypatch):
+    """16-bit tensors.  wide: fp32 arithmetic on the exact 16-bit inputs, each gradient
+    rounded once: |g - g64| <= eps |g64| + 1e-5 max|g64|.  fused: P and dS enter the MFMAs
+    as 16-bit values: max|g - g64| <= 8 eps max|g64| (an indexing mistake is O(1))."""
+    if path == "wide":
+        monkeypatch.setenv("GEV2_ATTN_BWD_WIDE", "1")
+    else:
+        monkeypatch.delenv("GEV2_ATTN_BWD_WIDE", raising=False)
+    B, H, M, N, D, causal, mk = case
     Q, K, V = _qkv(27, B, H, M, N, D, dtype)
     dY = rounded(np.random.default_rng(28).standard_normal(Q.shape), dtype).astype(np.float32)
     mask = _mask(mk, B, M, N, 29)
@@ -169,4 +187,8 @@ def test_16bit_backward(capi, dtype, causal, mk):
     for name, buf, a in zip(("dQ", "dK", "dV"), outs, (Q, K, V)):
         g = capi.from_storage(buf.download(a.shape, st), dtype)
         r = ref[name]
-        assert np.all(np.abs(g - r) <= eps * np.abs(r) + 1e-5 * np.abs(r).max()), name
+        if path == "wide":
+            assert np.all(np.abs(g - r) <= eps * np.abs(r) + 1e-5 * np.abs(r).max()), name
+        else:
+            err = float(np.abs(g - r).max())
+            assert err <= 8 * eps * np.abs(r).max(), (name, err, float(np.abs(r).max()))
