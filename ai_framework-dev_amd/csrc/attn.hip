@@ -44,7 +44,8 @@ struct AttnArgs {
   const void* K;
   const void* V;
   void* Y;
-  float* lse;            // [BH, M] natural-log sum of exp, optional
+  float* lse;            // [BH, lse_ld] natural-log sum of exp, optional
+  int lse_ld;            // rows per head in lse (M; the backward pads it to a multiple of 64)
   const void* mask;      // [B, M, N] (broadcast over H), optional
   int mask_kind;         // GEV2_MASK_*
   int BH, H, M, N;
@@ -329,7 +330,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
       w[1] = pack2(Elem<T>::bits(o[qt][dt][2] * inv), Elem<T>::bits(o[qt][dt][3] * inv));
       *reinterpret_cast<u32x2*>(yrow + 16 * dt + 4 * g) = w;
     }
-    if (a.lse && g == 0) a.lse[qhead + q[qt]] = (m_run[qt] + log2f(l)) * 0.69314718055994531f;
+    if (a.lse && g == 0) a.lse[(int64_t)bh * a.lse_ld + q[qt]] = (m_run[qt] + log2f(l)) * 0.69314718055994531f;
   }
 }
 
@@ -443,16 +444,24 @@ struct AttnBwdArgs {
   void* dV;
 };
 
+// 8 lanes per row, 16 bytes each per step
 template <typename T>
 __global__ void __launch_bounds__(256) attn_bwd_dot_kernel(const T* __restrict__ dO, const T* __restrict__ O,
-                                                           float* __restrict__ Dq, int64_t rows, int D) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+                                                           float* __restrict__ Dq, int64_t rows, int D, int M,
+                                                           int ld) {
+  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
   if (row >= rows) return;
   float acc = 0.f;
-  for (int d = lane; d < D; d += 64) acc += Elem<T>::load1(dO + row * D + d) * Elem<T>::load1(O + row * D + d);
-  for (int o = 32; o > 0; o >>= 1) acc = xor_sum(acc, o);
-  if (lane == 0) Dq[row] = acc;
+  for (int d = sub * 8; d < D; d += 64) {
+    float a[8], b[8];
+    chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(dO + row * D + d), a);
+    chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(O + row * D + d), b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += a[i] * b[i];
+  }
+  acc = xor_sum(xor_sum(xor_sum(acc, 1), 2), 4);
+  if (sub == 0) Dq[(row / M) * ld + row % M] = acc;
 }
 
 // 16-byte row piece (8 elements from 8 * chunk) of a tile whose rows hold
@@ -532,6 +541,8 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
   constexpr int KS = D / 32, DT = D / 16, RB = D * 2, TILE = 64 * RB;
   constexpr int NL = 2 * (TILE / 1024 / 4);          // loads per wave per query block (Q and dO)
   __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];
+  // lse and Dq of a query block (first 256 bytes of each 1 KB load), wave 0's two extra loads
+  __shared__ __attribute__((aligned(1024))) float aux[2][2][256];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -566,19 +577,34 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
   // causal without other masks: query blocks wholly before this block's first key see none of it
   const int qb0 = (!MASKED && a.causal) ? min(nqb, (kb * 64) / 64) : 0;
   const i32x4_t rQ = rsrc_words(a.Q), rO = rsrc_words(ba.dO);
+  const i32x4_t rL = rsrc_words(a.lse), rD = rsrc_words(ba.Dq);
   const uint32_t base = lds_addr(&lds[0][0][0]);
+  const uint32_t abase = lds_addr(&aux[0][0][0]);
   auto q_lds = [&](int st) { return base + st * 2 * TILE; };
   auto o_lds = [&](int st) { return base + st * 2 * TILE + TILE; };
+  // lse / Dq rows [q0, q0 + 64) of this head: 16 lanes x 4 floats; the arrays are padded to
+  // lse_ld (a multiple of 64) rows per head, so every piece is inside them
+  auto load_aux = [&](int q0, int st) {
+    const int off = lane < 16 ? static_cast<int>(((int64_t)bh * a.lse_ld + q0 + 4 * lane) * 4) : kOobOffset;
+    dma16(rL, off, 0, abase + st * 2048);
+    dma16(rD, off, 0, abase + st * 2048 + 1024);
+  };
   if (qb0 < nqb) {
     load_rows_b32swz<D>(rQ, qhead, qb0 * 64, a.M, wave, lane, q_lds(0));
     load_rows_b32swz<D>(rO, qhead, qb0 * 64, a.M, wave, lane, o_lds(0));
+    if (wave == 0) load_aux(qb0 * 64, 0);
   }
   for (int qb = qb0; qb < nqb; ++qb) {
     const int st = (qb - qb0) & 1;
     if (qb + 1 < nqb) {
       load_rows_b32swz<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
       load_rows_b32swz<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
-      __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+      if (wave == 0) {
+        load_aux((qb + 1) * 64, st ^ 1);
+        __builtin_amdgcn_s_waitcnt(0x3f70 | ((NL + 2) & 0xf) | (((NL + 2) >> 4) << 14));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+      }
     } else {
       __builtin_amdgcn_s_waitcnt(0x3f70);
     }
@@ -586,6 +612,8 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
     asm volatile("" ::: "memory");
     const char* ql = &lds[st][0][0];
     const char* ol = &lds[st][1][0];
+    const float* lsel = &aux[st][0][0];
+    const float* dql = &aux[st][1][0];
     uint32_t pw[4][2], sw[4][2];                      // P and dS of each 16-query tile, packed pairs
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -600,18 +628,20 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
       for (int r = 0; r < 4; ++r) {
         const int q = qb * 64 + 16 * t + 4 * g + r;   // row of this accumulator entry
         const bool q_ok = q < a.M;
-        const float lse2 = q_ok ? a.lse[qhead + q] * kLog2e : INFINITY;
-        const float dq = q_ok ? ba.Dq[qhead + q] : 0.f;
+        // rows past M hold padding (never-written lse / Dq): their P and dS are set to 0 outright
+        const float lse2 = lsel[16 * t + 4 * g + r] * kLog2e;
+        const float dq = dql[16 * t + 4 * g + r];
         float pv;
         if constexpr (MASKED) {
-          const float x = (key_ok && q_ok) ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : -INFINITY;
-          pv = __builtin_amdgcn_exp2f(x - lse2);
-          const bool m = (key_ok && q_ok) ? masked_entry(a, b, q, key) : true;
+          const bool in = key_ok && q_ok;
+          const float x = in ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : 0.f;
+          pv = in ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
+          const bool m = in ? masked_entry(a, b, q, key) : true;
           ds[r] = m ? 0.f : pv * (pacc[r] - dq);
         } else {
           const bool live = key_ok && q_ok && !(a.causal && key > q);
           pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
-          ds[r] = pv * (pacc[r] - dq);
+          ds[r] = live ? pv * (pacc[r] - dq) : 0.f;
         }
         p[r] = pv;
       }
@@ -681,8 +711,8 @@ __global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnBwdArgs ba) {
   }
   const float kLog2e = 1.4426950408889634f;
   const float xscale = a.scale * kLog2e;
-  const float lse2 = q_ok ? a.lse[qhead + q] * kLog2e : INFINITY;
-  const float dq = q_ok ? ba.Dq[qhead + q] : 0.f;
+  const float lse2 = q_ok ? a.lse[(int64_t)bh * a.lse_ld + q] * kLog2e : INFINITY;
+  const float dq = q_ok ? ba.Dq[(int64_t)bh * a.lse_ld + q] : 0.f;
   __builtin_amdgcn_s_waitcnt(0x3f70);
   asm volatile("" ::: "memory");
 
@@ -727,14 +757,15 @@ __global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnBwdArgs ba) {
         const int key = kb * 64 + 16 * kt + 4 * g + r;
         const bool key_ok = key < a.N;
         if constexpr (MASKED) {
-          const float x = (key_ok && q_ok) ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : -INFINITY;
-          const float pv = __builtin_amdgcn_exp2f(x - lse2);
-          const bool m = (key_ok && q_ok) ? masked_entry(a, b, q, key) : true;
+          const bool in = key_ok && q_ok;
+          const float x = in ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : 0.f;
+          const float pv = in ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
+          const bool m = in ? masked_entry(a, b, q, key) : true;
           ds[r] = m ? 0.f : pv * (pacc[r] - dq);
         } else {
           const bool live = key_ok && q_ok && !(a.causal && key > q);
           const float pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
-          ds[r] = pv * (pacc[r] - dq);
+          ds[r] = live ? pv * (pacc[r] - dq) : 0.f;
         }
       }
       sw[kt][0] = pack2(Elem<T>::bits(ds[0]), Elem<T>::bits(ds[1]));
@@ -764,8 +795,9 @@ template <typename T, int D>
 hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
   const AttnArgs& a = ba.f;
   const int64_t rows = (int64_t)a.BH * a.M;
-  hipLaunchKernelGGL((attn_bwd_dot_kernel<T>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s,
-                     static_cast<const T*>(ba.dO), static_cast<const T*>(a.Y), const_cast<float*>(ba.Dq), rows, D);
+  hipLaunchKernelGGL((attn_bwd_dot_kernel<T>), dim3(static_cast<unsigned>((rows + 31) / 32)), dim3(256), 0, s,
+                     static_cast<const T*>(ba.dO), static_cast<const T*>(a.Y), const_cast<float*>(ba.Dq), rows, D,
+                     a.M, a.lse_ld);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const bool masked = a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f);
@@ -892,9 +924,11 @@ int64_t widened_bytes(int64_t BH, int64_t M, int64_t N, int64_t D) {
 
 int64_t align256(int64_t n) { return ((n + 255) / 256) * 256; }
 
-// fused 16-bit backward: O [BH, M, D] (16-bit), lse and Dq [BH, M] fp32
+// fused 16-bit backward: O [BH, M, D] (16-bit), lse and Dq [BH, Mp] fp32 with
+// Mp = M rounded up to 64 (whole 64-row pieces per head)
+int64_t padded_rows(int64_t M) { return (M + 63) / 64 * 64; }
 int64_t fused_bwd_bytes(int64_t BH, int64_t M, int64_t D) {
-  return align256(BH * M * D * 2) + 2 * align256(BH * M * 4);
+  return align256(BH * M * D * 2) + 2 * align256(BH * padded_rows(M) * 4);
 }
 
 // the fused backward unless GEV2_ATTN_BWD_WIDE=1 (comparison runs)
@@ -922,7 +956,7 @@ int gev2_sdpa_fwd(const gev2_sdpa_desc* d, void* stream) {
   if (!d->Q || !d->K || !d->V) return attn_fail(GEV2_MISSING_INPUT, "Q / K / V is null");
   if (!d->Y) return attn_fail(GEV2_MISSING_OUTPUT, "Y is null");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  a.Q = d->Q; a.K = d->K; a.V = d->V; a.Y = d->Y; a.lse = d->lse;
+  a.Q = d->Q; a.K = d->K; a.V = d->V; a.Y = d->Y; a.lse = d->lse; a.lse_ld = d->M;
   const int64_t M = d->M, N = d->N, D = d->D;
   if (fused_ok(d->dtype, d->D)) {
     if (reinterpret_cast<uintptr_t>(d->Q) % 16 || reinterpret_cast<uintptr_t>(d->Y) % 16 ||
@@ -968,10 +1002,11 @@ int gev2_sdpa_bwd(const gev2_sdpa_bwd_desc* d, void* stream) {
       return attn_fail(GEV2_INVALID, "fused path needs Q / K / V / dY under 2^31 bytes");
     char* w = static_cast<char*>(d->workspace);
     void* O = w;
+    const int64_t Mp = padded_rows(M);
     float* lse = reinterpret_cast<float*>(w + align256(BH * M * D * 2));
-    float* Dq = reinterpret_cast<float*>(w + align256(BH * M * D * 2) + align256(BH * M * 4));
+    float* Dq = reinterpret_cast<float*>(w + align256(BH * M * D * 2) + align256(BH * Mp * 4));
     gev2::AttnArgs fa = a;
-    fa.Q = d->Q; fa.K = d->K; fa.V = d->V; fa.Y = O; fa.lse = lse;
+    fa.Q = d->Q; fa.K = d->K; fa.V = d->V; fa.Y = O; fa.lse = lse; fa.lse_ld = static_cast<int>(Mp);
     hipError_t e;
     if (d->dtype == GEV2_BF16) e = D == 64 ? gev2::launch_attn_fwd<__bf16, 64>(fa, s) : gev2::launch_attn_fwd<__bf16, 128>(fa, s);
     else e = D == 64 ? gev2::launch_attn_fwd<_Float16, 64>(fa, s) : gev2::launch_attn_fwd<_Float16, 128>(fa, s);

@@ -293,9 +293,10 @@ const char* gev2_rnn_last_error(void);
  * Forward, F16 / BF16 with D = 64 or 128: one fused kernel, no workspace;
  * `lse` (optional, fp32 [B,H,M]) receives each row's log-sum-exp.
  * Forward, F32: S / P in `workspace` (gev2_sdpa_workspace_size bytes).
- * Backward: the reference's algorithm batched over all (b, h) slices in fp32,
- * with P and dP in `workspace`; 16-bit tensors are widened to fp32 copies in
- * the same workspace and the gradients rounded back.
+ * Backward, F16 / BF16 with D = 64 or 128: fused kernels (P recomputed from
+ * the forward's row log-sum-exp, O(N) workspace).  Otherwise the reference's
+ * algorithm batched over all (b, h) slices in fp32, with P and dP in
+ * `workspace`.
  */
 enum { GEV2_MASK_NONE = 0, GEV2_MASK_I8 = 1, GEV2_MASK_I32 = 2, GEV2_MASK_F32 = 3 };
 
