@@ -7,6 +7,7 @@ Outputs (next to the Python package, like the reference's CMake output dir
   graph_executor_v2/ops/_ops_gemm*.so     pybind11: the GEMM op surface
   graph_executor_v2/ops/_ops_conv2d*.so   pybind11: conv2d on the GEMM op
   graph_executor_v2/ops/_ops_rnn*.so      pybind11: Elman RNN on the GEMM op
+  graph_executor_v2/ops/_ops_sdpa*.so     pybind11: scaled dot-product attention
 
 Usage: python ai_framework-dev_amd/build.py [--force] [-j N]
 """
@@ -46,8 +47,10 @@ BIND_SOURCES = {
     "_ops_gemm": ["bindings/gemm_pybind.cpp", "host/gemm_host.cpp"],
     "_ops_conv2d": ["bindings/conv2d_pybind.cpp", "host/conv2d_host.cpp"],
     "_ops_rnn": ["bindings/rnn_pybind.cpp", "host/rnn_host.cpp"],
+    "_ops_sdpa": ["bindings/sdpa_pybind.cpp", "host/sdpa_host.cpp"],
 }
-HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp", "host/rnn_host.hpp"]
+HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp", "host/rnn_host.hpp",
+                "host/sdpa_host.hpp"]
 
 
 def _newer(target: str, deps: list[str]) -> bool:
@@ -106,7 +109,7 @@ def build_bindings(force: bool, jobs: int) -> list[str]:
                    "-fvisibility=hidden",
                    f"-I{pybind11.get_include()}", f"-I{py_inc}", f"-I{INCLUDE}", f"-I{CSRC}",
                    *paths, "-o", out + ".tmp"]
-            if mod in ("_ops_gemm", "_ops_conv2d", "_ops_rnn"):
+            if mod in ("_ops_gemm", "_ops_conv2d", "_ops_rnn", "_ops_sdpa"):
                 cmd += [f"-L{OUT_DIR}", "-lgev2", "-Wl,-rpath,$ORIGIN"]
             cmds.append((cmd, out))
 

@@ -192,3 +192,42 @@ def test_16bit_backward(capi, dtype, case, path, monkeypatch):
         else:
             err = float(np.abs(g - r).max())
             assert err <= 8 * eps * np.abs(r).max(), (name, err, float(np.abs(r).max()))
+
+
+@pytest.fixture(scope="module")
+def host(gpu):
+    from graph_executor_v2.ops import _ops_sdpa as s
+    from graph_executor_v2.ops.device_array import DeviceArray
+    return s, DeviceArray
+
+
+@pytest.mark.parametrize("dtype,causal,mk", [(F32, False, O.MASK_I8), (BF16, True, O.MASK_NONE),
+                                             (F16, False, O.MASK_F32)], ids=["f32-i8", "bf16-causal", "f16-f32mask"])
+def test_host_api(capi, host, dtype, causal, mk):
+    """SDPACudaLaunch / SDPACudaBackwardLaunch (workspace allocated per call, as the
+    reference does) give what the C ABI gives."""
+    sd, DA = host
+    B, H, M, N, D = 1, 2, 48, 72, 64
+    Q, K, V = _qkv(33, B, H, M, N, D, dtype)
+    dY = rounded(np.random.default_rng(34).standard_normal(Q.shape), dtype).astype(np.float32) if dtype != F32 \
+        else np.random.default_rng(34).standard_normal(Q.shape).astype(np.float32)
+    mask = _mask(mk, B, M, N, 35)
+    name = {F32: "float32", BF16: "bfloat16", F16: "float16"}[dtype]
+    code = {F32: sd.DType.F32, BF16: sd.DType.BF16, F16: sd.DType.F16}[dtype]
+    dq, dk, dv, dy = (DA.from_numpy(a, name) for a in (Q, K, V, dY))
+    y = DA.empty(Q.shape, name)
+    gq, gk, gv = DA.empty(Q.shape, name), DA.empty(K.shape, name), DA.empty(V.shape, name)
+    mb = capi.DeviceBuffer.from_numpy(mask) if mask is not None else None
+    mdt = {O.MASK_I8: sd.DType.I8, O.MASK_I32: sd.DType.I32, O.MASK_F32: sd.DType.F32}.get(mk, sd.DType.I8)
+    a = sd.SDPAAttrs()
+    a.causal = causal
+    sd.forward(dq.ptr, list(Q.shape), dk.ptr, list(K.shape), dv.ptr, list(V.shape), y.ptr, list(Q.shape),
+               mask_ptr=mb.ptr if mb else None, mask_dtype=mdt, attrs=a, dtype=code)
+    sd.backward(dq.ptr, list(Q.shape), dk.ptr, list(K.shape), dv.ptr, list(V.shape), dy.ptr, dq_ptr=gq.ptr,
+                dk_ptr=gk.ptr, dv_ptr=gv.ptr, mask_ptr=mb.ptr if mb else None, mask_dtype=mdt, attrs=a, dtype=code)
+    Y64, _, _ = O.sdpa_forward(Q, K, V, causal=causal, mask=mask, mask_kind=mk)
+    ref = O.sdpa_backward(Q, K, V, dY, causal=causal, mask=mask, mask_kind=mk)
+    tol = 1e-4 if dtype == F32 else 8 * O.storage_eps(dtype)
+    assert np.abs(y.get() - Y64).max() <= tol * max(1.0, np.abs(Y64).max())
+    for g_, r in ((gq, ref["dQ"]), (gk, ref["dK"]), (gv, ref["dV"])):
+        assert np.abs(g_.get() - r).max() <= tol * max(1.0, np.abs(r).max())
