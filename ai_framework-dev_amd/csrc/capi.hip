@@ -425,21 +425,32 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   // gA[M,K] = alpha * dY' [M,N] * B^T : NT (prologue on A when fused)
   if (d->gA) {
     const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, K, batch, dt);
-    const int cfg = pick_cfg(dt, M, K, batch, fused);
-    gev2::TileArgs a{};
-    a.A = G; a.lda = ldG; a.sA = sG;
-    a.Zi = fused ? d->Z : nullptr; a.ldzi = ldz; a.sZi = d->stride_z;
-    a.B = d->B; a.ldb = ldb; a.sB = d->stride_b;
-    a.D = d->gA; a.ldd = ldga; a.sD = d->stride_ga;
-    a.M = static_cast<int>(M); a.N = static_cast<int>(K); a.K = static_cast<int>(N);
-    a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = d->alpha;
-    a.slope = d->leaky_slope; a.pro_act = d->act;
-    const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
-    a.tiles_m = static_cast<int>((M + bm - 1) / bm);
-    a.tiles_n = static_cast<int>((K + bn - 1) / bn);
-    a.store_vec = out_level(d->gA, ldga, d->stride_ga, M, K, batch, dt);
-    hipError_t e = gev2::launch_tile(dt, cfg, false, true, fused ? 1 : 0, vec, a, batch, s);
-    if (e != hipSuccess) return hip_fail(e, "dX launch");
+    if (M <= gev2::kSkinnyMaxM && batch == 1 && vec && env_int("GEV2_NO_SKINNY", 0) == 0) {
+      // one wave per output column, each reading one row of B
+      gev2::SkinnyNtArgs n{};
+      n.G = G; n.Z = fused ? d->Z : nullptr; n.B = d->B; n.D = d->gA;
+      n.ldg = ldG; n.ldz = ldz; n.ldb = ldb; n.ldd = ldga;
+      n.M = static_cast<int>(M); n.N = static_cast<int>(N); n.K = static_cast<int>(K);
+      n.act = d->act; n.slope = d->leaky_slope; n.alpha = d->alpha;
+      hipError_t e = gev2::launch_skinny_nt(dt, n, s);
+      if (e != hipSuccess) return hip_fail(e, "dX skinny launch");
+    } else {
+      const int cfg = pick_cfg(dt, M, K, batch, fused);
+      gev2::TileArgs a{};
+      a.A = G; a.lda = ldG; a.sA = sG;
+      a.Zi = fused ? d->Z : nullptr; a.ldzi = ldz; a.sZi = d->stride_z;
+      a.B = d->B; a.ldb = ldb; a.sB = d->stride_b;
+      a.D = d->gA; a.ldd = ldga; a.sD = d->stride_ga;
+      a.M = static_cast<int>(M); a.N = static_cast<int>(K); a.K = static_cast<int>(N);
+      a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = d->alpha;
+      a.slope = d->leaky_slope; a.pro_act = d->act;
+      const int bm = gev2::tile_bm(cfg, vec), bn = gev2::tile_bn(cfg, vec);
+      a.tiles_m = static_cast<int>((M + bm - 1) / bm);
+      a.tiles_n = static_cast<int>((K + bn - 1) / bn);
+      a.store_vec = out_level(d->gA, ldga, d->stride_ga, M, K, batch, dt);
+      hipError_t e = gev2::launch_tile(dt, cfg, false, true, fused ? 1 : 0, vec, a, batch, s);
+      if (e != hipSuccess) return hip_fail(e, "dX launch");
+    }
   }
   // gB[K,N] = alpha * A^T [K,M] * dY' [M,N] : TN (prologue on B + fused dBias when fused)
   if (d->gB) {

@@ -164,6 +164,64 @@ __global__ void __launch_bounds__(256) finish_col_sums_kernel(const float* parti
   if (g == 0 && n < N) gbias[(int64_t)bz * sGbias + n] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
 }
 
+// Skinny NT product for the backward's gA when M <= 16:
+//   D[m][k] = alpha * sum_n G[m][n] * (Z ? act'(Z[m][n]) : 1) * B[k][n].
+// Every output column k is a dot product of one contiguous row of B with the
+// M rows of G, so one wave per k reads that row once in 16-byte chunks (lanes
+// stride over n), keeps M partial sums, and adds them across the wave in a
+// fixed order; G (and Z) are small and come from L2.
+template <typename T>
+__global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
+  constexpr int EPC = Elem<T>::kPerChunk;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.x * 4 + wave;
+  if (k >= p.K) return;                              // wave-uniform; no barrier below
+  const T* G = reinterpret_cast<const T*>(p.G);
+  const T* Z = reinterpret_cast<const T*>(p.Z);
+  const T* brow = reinterpret_cast<const T*>(p.B) + (int64_t)k * p.ldb;
+  float acc[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+  for (int n0 = lane * EPC; n0 < p.N; n0 += 64 * EPC) {
+    float bv[EPC];
+    chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(brow + n0), bv);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      if (m >= p.M) break;
+      float gv[EPC];
+      chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0), gv);
+      if (Z) {
+        float zv[EPC];
+        chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n0), zv);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) gv[e] *= act_grad(zv[e], p.act, p.slope);
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) acc[m] = fmaf(gv[e], bv[e], acc[m]);
+    }
+  }
+  T* D = reinterpret_cast<T*>(p.D);
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    if (m >= p.M) break;
+    float v = acc[m];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) Elem<T>::store1(D + (int64_t)m * p.ldd + k, p.alpha * v);
+  }
+}
+
+hipError_t launch_skinny_nt(int dtype, const SkinnyNtArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.K + 3) / 4));
+  switch (dtype) {
+    case kF32: hipLaunchKernelGGL(skinny_nt_kernel<float>, grid, dim3(256), 0, s, a); break;
+    case kBF16: hipLaunchKernelGGL(skinny_nt_kernel<__bf16>, grid, dim3(256), 0, s, a); break;
+    case kF16: hipLaunchKernelGGL(skinny_nt_kernel<_Float16>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <typename T>
 static hipError_t grad_prep_t(const PrepArgs& a, int batch, hipStream_t s) {
   constexpr int COLS = 32 * Elem<T>::kPerChunk;

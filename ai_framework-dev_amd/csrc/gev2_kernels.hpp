@@ -70,6 +70,17 @@ struct PrepArgs {
   int act; float slope;
 };
 hipError_t launch_grad_prep(int dtype, const PrepArgs& a, int batch, hipStream_t s);
+
+// gA of the backward when M <= 16 (one slice): D[M,K] = alpha * (G (.) act'(Z)) B^T
+// with B [K,N]; Z null when G is already dY'.  Rows of G, Z and B must be
+// 16-byte aligned with N a multiple of the chunk.
+struct SkinnyNtArgs {
+  const void* G; const void* Z; const void* B; void* D;
+  int64_t ldg, ldz, ldb, ldd;
+  int M, N, K;
+  int act; float slope, alpha;
+};
+hipError_t launch_skinny_nt(int dtype, const SkinnyNtArgs& a, hipStream_t s);
 hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
                                   float* gbias, int64_t sGbias, int batch, hipStream_t s);
 

@@ -118,6 +118,11 @@ BWD_CASES = [
     (300, 260, 520, F16, "sigmoid", O.BIAS_PERN, True, False, False),  # dBias w/o dW
     (256, 512, 384, BF16, "relu", O.BIAS_PERN, True, True, True),
     (130, 200, 64, F32, "gelu", O.BIAS_NONE, False, True, False),
+    # M <= 16: gA on the skinny NT kernel (act' on the fly, or on a materialised dY')
+    (5, 384, 200, F32, "relu", O.BIAS_PERN, True, True, False),
+    (16, 1024, 1536, BF16, "tanh", O.BIAS_PERN, True, True, False),
+    (1, 64, 96, F16, "leakyrelu", O.BIAS_SCALAR, True, False, False),
+    (12, 520, 72, F32, "gelu", O.BIAS_PERM, True, True, True),
 ]
 
 
