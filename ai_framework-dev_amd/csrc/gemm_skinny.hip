@@ -226,8 +226,30 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4& a, const u32x4& b, const 
                                                   c, 0, 0, 0);
 }
 
-constexpr int kSplitCols = 256;   // W columns per workgroup (64 per wave)
-constexpr int kSplitRows = 256;   // W rows (K) per workgroup
+// W block per workgroup: COLS columns x ROWS rows, 128 KB (COLS 256 or 512);
+// wave w takes COLS / 4 columns over all ROWS rows.
+template <int COLS>
+struct SplitShape {
+  static constexpr int kCols = COLS;
+  static constexpr int kRows = 65536 / COLS;                 // 128 KB of 16-bit W
+  static constexpr int kWaveCols = COLS / 4;
+  static constexpr int kRowBytes = kWaveCols * 2;            // bytes per W row per wave
+  static constexpr int kTiles = kWaveCols / 16;              // 16-column MFMA tiles per wave
+  static constexpr int kSteps = kRows / 32;                  // k-steps of 32
+  static constexpr int kLoads = kRows * kRowBytes / 1024;    // W loads per wave (32)
+  static constexpr int kXBlocks = kRows / 8;                 // 8-k X blocks (16 rows x 16 B)
+  static constexpr int kXLoads = kXBlocks / 4 / 4;           // X loads per wave
+};
+
+// 256 columns unless GEV2_SKINNY_COLS=512 (the kernel, the reduction and the
+// workspace size all follow this choice).
+int skinny_split_cols() {
+  static const int c = [] {
+    const char* v = std::getenv("GEV2_SKINNY_COLS");
+    return (v && std::atoi(v) == 512) ? 512 : 256;
+  }();
+  return c;
+}
 
 template <typename T>
 __device__ __forceinline__ void skinny_out(const SkinnyArgs& p, int m, int n, float acc) {
@@ -244,45 +266,47 @@ __device__ __forceinline__ int64_t skinny_part_index(int split, int ntile, int t
   return ((int64_t)split * ntile + tile) * (16 * mq) + lane;
 }
 
-template <typename T>
+template <typename T, int COLS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
-  constexpr int RB = 128;                            // bytes per W row per wave (64 columns)
-  constexpr int NWL = kSplitRows * RB / 1024;        // W loads per wave (32)
-  constexpr int WBYTES = kSplitRows * RB;            // 32 KB per wave
-  constexpr int XBYTES = kSplitRows / 8 * 256;       // 8 KB: 32 k-blocks x 16 rows x 16 B
+  using S = SplitShape<COLS>;
+  constexpr int RB = S::kRowBytes;
+  constexpr int NWL = S::kLoads;
+  constexpr int WBYTES = S::kRows * RB;                      // 32 KB per wave
+  constexpr int XBYTES = S::kXBlocks * 256;
+  constexpr int RPL = 1024 / RB;                             // W rows per load
+  constexpr int BPR = RB / 32;                               // 32-byte blocks per row
   __shared__ __attribute__((aligned(1024))) char lds[4 * WBYTES + XBYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int slab = blockIdx.x % nslab, split = blockIdx.x / nslab;
-  const int c0 = slab * kSplitCols + wave * 64;      // this wave's first column
-  const int k0 = split * kSplitRows;
+  const int c0 = slab * S::kCols + wave * S::kWaveCols;      // this wave's first column
+  const int k0 = split * S::kRows;
   char* wl = lds + wave * WBYTES;
   char* xl = lds + 4 * WBYTES;
 
-  // X: load i (of 8, two per wave) fills k-blocks 4i .. 4i+3: lane -> block
-  // 4i + lane/16, row m = lane % 16
+  // X: load i fills k-blocks 4i .. 4i+3: lane -> block 4i + lane/16, row m = lane % 16
   const i32x4_t rX = rsrc_words(p.A);
   {
     const int m = lane & 15;
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int i = 2 * wave + ii;
+    for (int ii = 0; ii < S::kXLoads; ++ii) {
+      const int i = S::kXLoads * wave + ii;
       const int k = k0 + 8 * (4 * i + (lane >> 4));
       const int off = (m < p.M && k < p.K) ? static_cast<int>(((int64_t)m * p.lda + k) * sizeof(T)) : kOobOffset;
       dma16(rX, off, 0, lds_addr(xl) + i * 1024);
     }
   }
-  // W: load j fills rows 8j .. 8j+7 of this wave's 128-byte rows; the lane's
-  // 16 bytes hold logical 32-byte block (physical ^ (row & 3))
+  // W: load j fills rows RPL j .. of this wave's rows; the lane's 16 bytes hold
+  // logical 32-byte block (physical ^ (row & 3))
   const i32x4_t rW = rsrc_words(p.B);
   {
-    const int rsub = lane >> 3, pb = (lane & 7) >> 1, half = lane & 1;
+    const int rsub = lane / (2 * BPR), pb = (lane % (2 * BPR)) >> 1, half = lane & 1;
     const uint32_t wl_addr = lds_addr(wl);
 #pragma unroll
     for (int j = 0; j < NWL; ++j) {
-      const int row = 8 * j + rsub;
+      const int row = RPL * j + rsub;
       const int col = c0 + ((pb ^ (row & 3)) << 4) + half * 8;
       const int k = k0 + row;
       const int off = (k < p.K && col < p.N) ? static_cast<int>(((int64_t)k * p.ldb + col) * sizeof(T)) : kOobOffset;
@@ -292,24 +316,24 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
   __builtin_amdgcn_s_waitcnt(0x3f70 | (NWL & 0xf) | ((NWL >> 4) << 14));   // vmcnt(NWL): X loads done
   __syncthreads();                                                          // X block complete
 
-  f32x4_t acc[4];
+  f32x4_t acc[S::kTiles];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < S::kTiles; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // transpose reads: lane 16g + 4e + c addresses columns 16t + 4c.. of row
   // 32s + 8g + 4h + e
   const int g = lane >> 4, e = (lane >> 2) & 3, cq = lane & 3;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
-    // rows [128 half, 128 half + 128) are W loads [16 half, 16 half + 16)
+    // the first half of the rows are the first NWL / 2 W loads
     if (half == 0) __builtin_amdgcn_s_waitcnt(0x3f70 | (NWL / 2 & 0xf) | ((NWL / 2) >> 4 << 14));
     else __builtin_amdgcn_s_waitcnt(0x3f70);
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
-      const int s = 4 * half + ss;
+    for (int ss = 0; ss < S::kSteps / 2; ++ss) {
+      const int s = S::kSteps / 2 * half + ss;
       const u32x4 xa = *reinterpret_cast<const u32x4*>(xl + s * 1024 + lane * 16);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < S::kTiles; ++t) {
         u32x4 wf;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -329,7 +353,7 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
   const int nsplit = gridDim.x / nslab;
   if (nsplit == 1) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < S::kTiles; ++t) {
       const int n = c0 + 16 * t + (lane & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -341,8 +365,9 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
     const int mq = (p.M + 3) / 4;
     if (lane < 16 * mq) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        part[skinny_part_index(split, nslab * 16, slab * 16 + wave * 4 + t, lane, mq)] = acc[t];
+      for (int t = 0; t < S::kTiles; ++t)
+        part[skinny_part_index(split, nslab * (S::kCols / 16), slab * (S::kCols / 16) + wave * S::kTiles + t, lane,
+                               mq)] = acc[t];
     }
   }
 }
@@ -380,25 +405,34 @@ __global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArg
   }
 }
 
-template <typename T>
-static hipError_t launch_skinny_split(const SkinnyArgs& a, float* part, hipStream_t s) {
-  const int nslab = (a.N + kSplitCols - 1) / kSplitCols;
-  const int nsplit = (a.K + kSplitRows - 1) / kSplitRows;
+template <typename T, int COLS>
+static hipError_t launch_skinny_split_c(const SkinnyArgs& a, float* part, hipStream_t s) {
+  using S = SplitShape<COLS>;
+  const int nslab = (a.N + S::kCols - 1) / S::kCols;
+  const int nsplit = (a.K + S::kRows - 1) / S::kRows;
   f32x4_t* pv = reinterpret_cast<f32x4_t*>(part);
-  hipLaunchKernelGGL((gemm_skinny_split_kernel<T>), dim3(nslab * nsplit), dim3(256), 0, s, a, pv, nslab);
+  hipLaunchKernelGGL((gemm_skinny_split_kernel<T, COLS>), dim3(nslab * nsplit), dim3(256), 0, s, a, pv, nslab);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
-  const int64_t threads = (int64_t)nslab * 16 * 16 * ((a.M + 3) / 4);
+  const int ntile = nslab * (S::kCols / 16);
+  const int64_t threads = (int64_t)ntile * 16 * ((a.M + 3) / 4);
   hipLaunchKernelGGL((skinny_reduce_kernel<T>), dim3(static_cast<unsigned>((threads + kReduceThreads - 1) / kReduceThreads)),
-                     dim3(kReduceThreads), 0, s, a, pv, nsplit, nslab * 16);
+                     dim3(kReduceThreads), 0, s, a, pv, nsplit, ntile);
   return hipGetLastError();
 }
 
-// nsplit x nslab x 16 tiles x 16*ceil(M/4) lanes x 16 bytes
+template <typename T>
+static hipError_t launch_skinny_split(const SkinnyArgs& a, float* part, hipStream_t s) {
+  return skinny_split_cols() == 512 ? launch_skinny_split_c<T, 512>(a, part, s)
+                                    : launch_skinny_split_c<T, 256>(a, part, s);
+}
+
+// nsplit x (nslab x tiles per slab) x 16*ceil(M/4) lanes x 16 bytes
 int64_t skinny_split_workspace_bytes(int M, int N, int K) {
-  const int64_t nsplit = (K + kSplitRows - 1) / kSplitRows;
-  const int64_t nslab = (N + kSplitCols - 1) / kSplitCols;
-  return nsplit > 1 ? nsplit * nslab * 16 * 16 * ((M + 3) / 4) * 16 : 0;
+  const int cols = skinny_split_cols(), rows = 65536 / cols;
+  const int64_t nsplit = (K + rows - 1) / rows;
+  const int64_t nslab = (N + cols - 1) / cols;
+  return nsplit > 1 ? nsplit * nslab * (cols / 16) * 16 * ((M + 3) / 4) * 16 : 0;
 }
 
 // The split kernel takes 16-bit data with 16-byte aligned X rows spanning

@@ -11,6 +11,8 @@ device result must equal the oracle's after one rounding to the storage type,
 bit for bit (reference semantics: launcher.cu:147-274, epilogue traits.hpp:43-71).
 Shapes are ragged against every tile (M, N) and against BK = 32 and 64 (K).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -129,8 +131,11 @@ def test_skinny_explicit_workspace(gpu):
                 kw = dict(dtype=BF16, M=M, N=N, K=K, A=pX, B=pW, Y=pY, bias=pb, bias_kind=O.BIAS_PERN,
                           act="relu")
                 need = capi.fwd_workspace_size(**kw)
-                # K blocks x 256-column slabs x 16 tiles x 16*ceil(M/4) lanes x 16 bytes
-                assert need == -(-K // 256) * -(-N // 256) * 16 * 16 * -(-M // 4) * 16
+                # K blocks x column slabs x (cols / 16) tiles x 16*ceil(M/4) lanes x 16 bytes, for
+                # 256-column x 256-row W blocks (GEV2_SKINNY_COLS=512: 512 x 128)
+                cols = 512 if os.environ.get("GEV2_SKINNY_COLS") == "512" else 256
+                rows = 65536 // cols
+                assert need == -(-K // rows) * -(-N // cols) * (cols // 16) * 16 * -(-M // 4) * 16
                 if own:
                     kw.update(workspace=dev.empty(need), workspace_bytes=need)
                 capi.gemm_fwd(**kw)
