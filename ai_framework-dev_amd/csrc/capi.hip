@@ -334,6 +334,50 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   return GEV2_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Whether the backward materialises dY' = dY (.) act'(Z), and the scratch it
+// then needs: dY' (batch*M*N elements, 256-byte rounded) plus the PerN dBias
+// partials.  Shared by gev2_gemm_bwd and gev2_gemm_bwd_workspace_size.
+struct BwdScratch {
+  bool materialise{false}, prep_vec{false}, sums{false};
+  int row_blocks{0};
+  int64_t gz_bytes{0}, need{0};
+};
+
+BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
+  BwdScratch r;
+  const int64_t M = d->M, N = d->N, K = d->K;
+  const int batch = static_cast<int>(d->batch), dt = d->dtype;
+  const int64_t es = static_cast<int64_t>(elem_size(dt));
+  const int64_t ldgy = dense_ld(d->ldgy, N), ldz = dense_ld(d->ldz, N);
+  const bool scalar_loads = env_int("GEV2_SCALAR_LOADS", 0) != 0;
+  const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
+  const bool linear = d->act == GEV2_ACT_NONE || d->act == GEV2_ACT_RELU || d->act == GEV2_ACT_LEAKY_RELU;
+  const double work = static_cast<double>(M) * N * K * batch;
+  r.materialise = (!linear || work >= (1u << 30)) && (d->gA || d->gB) && env_int("GEV2_FUSED_BWD", 0) == 0;
+  if (!r.materialise) return r;
+  const int epc = elems_per_chunk(dt);
+  r.prep_vec = !scalar_loads && N % epc == 0 && vec_ok(d->gY, ldgy, d->stride_gy, N, M, batch, dt) &&
+               vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt);
+  r.sums = r.prep_vec && want_bias && d->bias_kind == GEV2_BIAS_PER_N;
+  r.row_blocks = static_cast<int>((M + gev2::kPrepRows - 1) / gev2::kPrepRows);
+  r.gz_bytes = ((static_cast<int64_t>(batch) * M * N * es + 255) / 256) * 256;
+  r.need = r.gz_bytes + (r.sums ? static_cast<int64_t>(batch) * r.row_blocks * N * 4 : 0);
+  return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t gev2_gemm_bwd_workspace_size(const gev2_gemm_bwd_desc* d) {
+  if (!d || check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch) != GEV2_OK) return -1;
+  return bwd_scratch(d).need;
+}
+
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   t_last_error.clear();
   if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
@@ -371,15 +415,12 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   int64_t ldG = ldgy, sG = d->stride_gy;
   bool fused = true;
   bool bias_done = false;
-  if ((!linear || work >= (1u << 30)) && (d->gA || d->gB) && env_int("GEV2_FUSED_BWD", 0) == 0) {
-    const int epc = elems_per_chunk(dt);
-    const bool prep_vec = !scalar_loads && N % epc == 0 && vec_ok(d->gY, ldgy, d->stride_gy, N, M, batch, dt) &&
-                          vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt);
-    const bool sums = prep_vec && want_bias && d->bias_kind == GEV2_BIAS_PER_N;
-    const int row_blocks = static_cast<int>((M + gev2::kPrepRows - 1) / gev2::kPrepRows);
-    const int64_t gz_bytes = ((static_cast<int64_t>(batch) * M * N * es + 255) / 256) * 256;
-    const int64_t part_bytes = sums ? static_cast<int64_t>(batch) * row_blocks * N * 4 : 0;
-    const int64_t need = gz_bytes + part_bytes;
+  const BwdScratch sc = bwd_scratch(d);
+  if (sc.materialise) {
+    const bool prep_vec = sc.prep_vec, sums = sc.sums;
+    const int row_blocks = sc.row_blocks;
+    const int64_t gz_bytes = sc.gz_bytes;
+    const int64_t need = sc.need;
     void* ws = nullptr;
     if (d->workspace && d->workspace_bytes >= need && (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
       ws = d->workspace;

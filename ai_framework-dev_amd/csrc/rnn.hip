@@ -19,6 +19,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <mutex>
+#include <set>
 #include <string>
 
 #include "../../include/gev2_gemm.h"
@@ -206,6 +211,83 @@ int hip_status(hipError_t e, const char* where) {
   return GEV2_HIP_ERROR;
 }
 
+// The step loops are T serial launches of small kernels, which the launch rate
+// bounds.  On a created stream each distinct (descriptor, stream) is run
+// eagerly the first time (which also creates the operator's per-stream
+// scratch), recorded into a HIP graph the second time, and replayed from then
+// on.  A replay reads the buffers the descriptor names, as they are at launch.
+// GEV2_RNN_GRAPH=0 turns this off.  At most kMaxGraphs executables are kept.
+constexpr size_t kMaxGraphs = 32;
+
+struct GraphCache {
+  std::mutex mu;
+  std::set<std::string> seen;
+  std::list<std::pair<std::string, hipGraphExec_t>> lru;   // most recent first
+};
+
+GraphCache& graph_cache() {
+  static GraphCache* c = new GraphCache();   // kept until exit (executables are per process)
+  return *c;
+}
+
+bool graphs_on() {
+  static const bool on = [] {
+    const char* v = std::getenv("GEV2_RNN_GRAPH");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
+// `graph_ok`: every operator call of the loop runs on the descriptor's own
+// scratch (or needs none), so a recorded graph names no per-stream buffer
+// that a later call on the stream could reallocate.
+template <typename Desc, typename Fn>
+int run_cached(const Desc* d, char dir, hipStream_t s, bool graph_ok, Fn&& work) {
+  if (!s || !graph_ok || !graphs_on()) return work();
+  std::string key(1, dir);
+  key.append(reinterpret_cast<const char*>(d), sizeof(Desc));
+  key.append(reinterpret_cast<const char*>(&s), sizeof(s));
+  GraphCache& c = graph_cache();
+  bool first = false;
+  {
+    std::lock_guard<std::mutex> lk(c.mu);
+    for (auto it = c.lru.begin(); it != c.lru.end(); ++it) {
+      if (it->first == key) {
+        c.lru.splice(c.lru.begin(), c.lru, it);
+        return hip_status(hipGraphLaunch(it->second, s), "rnn graph launch");
+      }
+    }
+    first = c.seen.insert(key).second;
+    if (first && c.seen.size() > 4 * kMaxGraphs) {
+      c.seen.clear();
+      c.seen.insert(key);
+    }
+  }
+  if (first) return work();                  // first sighting: eager
+  {
+    int st = hip_status(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "rnn graph capture");
+    if (st != GEV2_OK) return st;
+    st = work();
+    hipGraph_t g = nullptr;
+    const hipError_t ee = hipStreamEndCapture(s, &g);
+    if (st != GEV2_OK || ee != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return st != GEV2_OK ? st : hip_status(ee, "rnn graph capture");
+    }
+    hipGraphExec_t ex = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) return hip_status(ie, "rnn graph instantiate");
+    std::lock_guard<std::mutex> lk(c.mu);
+    c.lru.emplace_front(key, ex);
+    if (c.lru.size() > kMaxGraphs) {
+      (void)hipGraphExecDestroy(c.lru.back().second);
+      c.lru.pop_back();
+    }
+    return hip_status(hipGraphLaunch(ex, s), "rnn graph launch");
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -224,6 +306,18 @@ int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
   const gev2::RnnDims dm{d->N, d->T, d->I, d->H};
   const int64_t es = esize(d->dtype), IH = d->I + d->H;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  bool graph_ok;
+  {
+    gev2_gemm_fwd_desc f{};
+    f.dtype = d->dtype; f.act = d->act; f.alpha = 1.f; f.bias_kind = d->bias ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+    f.M = d->N; f.N = d->H; f.K = IH; f.batch = 1;
+    f.A = d->xh; f.lda = IH; f.B = d->wcat; f.ldb = d->H; f.bias = d->bias;
+    f.Y = d->Y; f.ldy = (int64_t)d->T * d->H;
+    const int64_t need = gev2_gemm_fwd_workspace_size(&f);
+    graph_ok = need == 0 || (need > 0 && d->ws && d->ws_bytes >= need);
+  }
+  return run_cached(d, 'f', s, graph_ok, [&]() -> int {
+  int st = GEV2_OK;
   // wcat = [Wx ; Wh]  ([I+H, H])
   st = hip_status(hipMemcpyAsync(d->wcat, d->Wx, (size_t)d->I * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wx");
   if (st != GEV2_OK) return st;
@@ -250,6 +344,7 @@ int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
     if (st != GEV2_OK) return st;
   }
   return GEV2_OK;
+  });
 }
 
 int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
@@ -271,6 +366,23 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
     if (st == GEV2_OK) st = hip_status(gev2::launch_zero<float>(d->dB, d->H, s), "zero");
     return st;
   }
+  bool graph_ok;
+  {
+    gev2_gemm_bwd_desc b{};
+    b.dtype = d->dtype; b.act = d->act; b.alpha = 1.f; b.bias_kind = d->dB ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+    b.M = d->N; b.N = d->H; b.K = IH; b.batch = 1;
+    b.A = d->xh; b.lda = IH; b.B = d->wcat; b.ldb = d->H; b.gY = d->g; b.ldgy = d->H;
+    b.Z = d->Z; b.ldz = (int64_t)d->T * d->H;
+    b.gA = d->dxh; b.ldga = IH; b.gB = (d->dWx || d->dWh) ? d->tmpw : nullptr; b.ldgb = d->H;
+    b.gBias = d->dB ? d->gb : nullptr;
+    const int64_t need = gev2_gemm_bwd_workspace_size(&b);
+    // every step's Z slice (Z + t*H) must share the alignment the size was computed for
+    graph_ok = (d->H * es) % 16 == 0 &&
+               (need == 0 || (need > 0 && d->ws && d->ws_bytes >= need &&
+                              (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0));
+  }
+  return run_cached(d, 'b', s, graph_ok, [&]() -> int {
+  int st = GEV2_OK;
   st = hip_status(hipMemcpyAsync(d->wcat, d->Wx, (size_t)d->I * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wx");
   if (st != GEV2_OK) return st;
   st = hip_status(hipMemcpyAsync(static_cast<char*>(d->wcat) + (size_t)d->I * d->H * es, d->Wh,
@@ -305,6 +417,7 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
   st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_finish, d->dxh, d->dwcat, d->dX, d->dh0, d->dWx,
                                     d->dWh, dm, s), "finish");
   return st;
+  });
 }
 
 }  // extern "C"

@@ -31,6 +31,7 @@ EXPORTED = [
     "gev2_rnn_fwd", "gev2_rnn_bwd", "gev2_rnn_last_error",
     "gev2_sdpa_fwd", "gev2_sdpa_bwd", "gev2_sdpa_workspace_size", "gev2_sdpa_last_error",
     "gev2_graph_begin", "gev2_graph_end", "gev2_graph_launch", "gev2_graph_destroy",
+    "gev2_gemm_bwd_workspace_size",
 ]
 
 
@@ -200,6 +201,8 @@ def lib() -> ctypes.CDLL:
     L.gev2_rnn_bwd.argtypes = [ctypes.POINTER(RnnBwdDesc), vp]
     L.gev2_rnn_last_error.restype = ctypes.c_char_p
     L.gev2_rnn_last_error.argtypes = []
+    L.gev2_gemm_bwd_workspace_size.restype = ctypes.c_int64
+    L.gev2_gemm_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdDesc)]
     L.gev2_graph_begin.argtypes = [vp]
     L.gev2_graph_end.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p)]
     L.gev2_graph_launch.argtypes = [vp, vp]

@@ -145,6 +145,11 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* desc, void* stream);
  * descriptor.  No counterpart in the reference (its forward needs none). */
 int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* desc);
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
+/* Scratch bytes gev2_gemm_bwd uses for `desc` (0: none, dY' is formed while
+ * loading); -1 for an invalid descriptor.  A `workspace` this large (256-byte
+ * aligned) keeps the call off the per-stream buffer.  No counterpart in the
+ * reference (its scratch is GemmWorkspace::scratch, sized by the caller). */
+int64_t gev2_gemm_bwd_workspace_size(const gev2_gemm_bwd_desc* desc);
 
 /*
  * 2-D convolution, NCHW, groups = 1, on the operator (replaces

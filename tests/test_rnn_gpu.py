@@ -143,3 +143,80 @@ def test_rnn_bf16(env, shape):
     for k in ("dWx", "dWh", "dB", "dh0", "dX"):
         rel = np.abs(out[k] - ref[k]).max() / max(1e-6, np.abs(ref[k]).max())
         assert rel <= 0.05, (k, rel)
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_rnn_graph_replays(env, dtype):
+    """On a created stream with the scratch in the descriptor, the step loops are recorded into
+    a HIP graph on the second call and replayed after: every call (eager, recording, replays),
+    each with new inputs and eager work between, equals an eager run bit for bit."""
+    import ctypes
+    from graph_executor_v2.ops import capi
+    N, T, I, H = 8, 6, 256, 256
+    es = capi.elem_bytes(dtype)
+    r = np.random.default_rng(16)
+    L = capi.lib()
+    bufs = []
+
+    def buf(nbytes):
+        b = capi.DeviceBuffer(max(nbytes, 16))
+        bufs.append(b)
+        return b.ptr
+
+    def put(a):
+        b = capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype))
+        bufs.append(b)
+        return b
+
+    X0, Wx, Wh, h0, b, dY0 = _inputs(17, N, T, I, H)
+    gX, gWx, gWh, gh0, gdY = (put(a) for a in (X0, Wx, Wh, h0, dY0))
+    gb = capi.DeviceBuffer.from_numpy(b)
+    bufs.append(gb)
+    IH = I + H
+    ws_bytes = 4 << 20
+
+    def descs():
+        Y, Z = buf(N * T * H * es), buf(N * T * H * es)
+        ws = buf(ws_bytes)
+        fd = capi.RnnDesc(dtype=dtype, act=capi.ACT["tanh"], save_z=1, N=N, T=T, I=I, H=H, X=gX.ptr, Wx=gWx.ptr,
+                          Wh=gWh.ptr, bias=gb.ptr, h0=gh0.ptr, Y=Y, Z=Z, xh=buf(N * IH * es), wcat=buf(IH * H * es),
+                          ws=ws, ws_bytes=ws_bytes)
+        out = {k: buf(n) for k, n in (("dWx", I * H * es), ("dWh", H * H * es), ("dB", H * 4), ("dh0", N * H * es),
+                                      ("dX", N * T * I * es))}
+        bd = capi.RnnBwdDesc(dtype=dtype, act=capi.ACT["tanh"], N=N, T=T, I=I, H=H, X=gX.ptr, Wx=gWx.ptr, Wh=gWh.ptr,
+                             h0=gh0.ptr, dY=gdY.ptr, Z=Z, xh=buf(N * IH * es), g=buf(N * H * es),
+                             wcat=buf(IH * H * es), dxh=buf(N * IH * es), dwcat=buf(IH * H * 4),
+                             tmpw=buf(IH * H * es), gb=buf(H * 4), ws=ws, ws_bytes=ws_bytes, **out)
+        return fd, bd, dict(Y=(Y, (N, T, H)), Z=(Z, (N, T, H)), **{k: (v, None) for k, v in out.items()})
+
+    st = capi.to_storage(np.zeros(1, np.float32), dtype).dtype
+
+    def read(ptrs):
+        capi.synchronize()
+        shapes = dict(Y=(N, T, H), Z=(N, T, H), dWx=(I, H), dWh=(H, H), dB=(H,), dh0=(N, H), dX=(N, T, I))
+        out = {}
+        for k, (p, _) in ptrs.items():
+            a = np.empty(shapes[k], np.float32 if k == "dB" else st)
+            capi.check(L.gev2_memcpy_dtoh(a.ctypes.data, p, a.nbytes), "dtoh")
+            out[k] = a
+        return out
+
+    stream = capi.Stream()
+    gfd, gbd, gptr = descs()          # graph-mode descriptors (created stream)
+    efd, ebd, eptr = descs()          # eager reference (null stream)
+    try:
+        for call in range(4):
+            X = r.standard_normal((N, T, I)).astype(np.float32)
+            dY = r.standard_normal((N, T, H)).astype(np.float32)
+            gX.upload(capi.to_storage(X, dtype))
+            gdY.upload(capi.to_storage(dY, dtype))
+            capi.check_rnn(L.gev2_rnn_fwd(ctypes.byref(gfd), stream.ptr), "fwd graph")
+            capi.check_rnn(L.gev2_rnn_bwd(ctypes.byref(gbd), stream.ptr), "bwd graph")
+            stream.synchronize()
+            capi.check_rnn(L.gev2_rnn_fwd(ctypes.byref(efd), None), "fwd eager")
+            capi.check_rnn(L.gev2_rnn_bwd(ctypes.byref(ebd), None), "bwd eager")
+            got, ref = read(gptr), read(eptr)
+            for k in got:
+                assert np.array_equal(got[k], ref[k]), (call, k)
+    finally:
+        stream.destroy()
