@@ -411,7 +411,7 @@ def skinny_cfg(ctx, iters, sets=10):
             "frac_hbm": byt / (ms * 1e-3) / 1e9 / PEAK_HBM, "path": path}
 
 
-def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=40):
+def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=200):
     """fp32 NumPy forward+backward (the reference's CPU path) on the full C3 step,
     repeated until about min_seconds of CPU work; the median step is reported."""
     from oracle import gemm_oracle as O
@@ -437,7 +437,7 @@ def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=40):
     return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": int(threads),
             "kind": "port",
             "sample": f"fp32 numpy forward+backward (np.matmul via {blas}) of the full {M}x{K} @ "
-                      f"{K}x{N} ReLU step, {len(ts)} repetitions ({sum(ts):.1f} s of CPU work), "
+                      f"{K}x{N} ReLU step, {len(ts)} repetitions ({sum(ts):.1f} s wall on {threads} threads), "
                       f"median {t * 1e3:.1f} ms per step"}
 
 
