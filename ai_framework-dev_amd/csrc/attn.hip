@@ -959,9 +959,9 @@ int gev2_sdpa_fwd(const gev2_sdpa_desc* d, void* stream) {
   a.Q = d->Q; a.K = d->K; a.V = d->V; a.Y = d->Y; a.lse = d->lse; a.lse_ld = d->M;
   const int64_t M = d->M, N = d->N, D = d->D;
   if (fused_ok(d->dtype, d->D)) {
-    if (reinterpret_cast<uintptr_t>(d->Q) % 16 || reinterpret_cast<uintptr_t>(d->Y) % 16 ||
-        a.BH * N * D * 2 > 0x7fffff00LL)
-      return attn_fail(GEV2_INVALID, "fused path needs 16-byte aligned Q / Y and K / V under 2^31 bytes");
+    for (const void* p : {d->Q, d->K, d->V, static_cast<const void*>(d->Y)})
+      if (reinterpret_cast<uintptr_t>(p) % 16) return attn_fail(GEV2_INVALID, "fused path needs 16-byte aligned tensors");
+    if (a.BH * N * D * 2 > 0x7fffff00LL) return attn_fail(GEV2_INVALID, "fused path needs K / V under 2^31 bytes");
     hipError_t e;
     if (d->dtype == GEV2_BF16) e = d->D == 64 ? gev2::launch_attn_fwd<__bf16, 64>(a, s) : gev2::launch_attn_fwd<__bf16, 128>(a, s);
     else e = d->D == 64 ? gev2::launch_attn_fwd<_Float16, 64>(a, s) : gev2::launch_attn_fwd<_Float16, 128>(a, s);
