@@ -23,6 +23,7 @@ GEOMS = {
     "c5a-like": dict(N=3, Cin=8, H=10, W=12, Cout=16, Kh=3, Kw=3, stride=(1, 1), pad=(1, 1), dil=(1, 1)),
     "stride2": dict(N=2, Cin=5, H=11, W=9, Cout=12, Kh=3, Kw=2, stride=(2, 1), pad=(0, 2), dil=(1, 1)),
     "dilated": dict(N=2, Cin=4, H=9, W=10, Cout=8, Kh=2, Kw=3, stride=(1, 2), pad=(1, 0), dil=(2, 1)),
+    "pointwise": dict(N=2, Cin=6, H=5, W=7, Cout=4, Kh=1, Kw=1, stride=(1, 1), pad=(0, 0), dil=(1, 1)),
 }
 
 

@@ -70,7 +70,8 @@ def _inputs(seed, N, T, I, H):
 
 
 @pytest.mark.parametrize("act", ACTS)
-@pytest.mark.parametrize("shape", [(4, 6, 24, 32), (40, 5, 48, 64)], ids=["skinny-N4", "tile-N40"])
+@pytest.mark.parametrize("shape", [(4, 6, 24, 32), (40, 5, 48, 64), (3, 1, 16, 32)], ids=["skinny-N4", "tile-N40",
+                                                                                     "one-step"])
 def test_rnn_f32(env, act, shape):
     N, T, I, H = shape
     X, Wx, Wh, h0, b, dY = _inputs(11, N, T, I, H)
