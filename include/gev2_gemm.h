@@ -229,6 +229,11 @@ const char* gev2_conv2d_last_error(void);
  * Workspaces (elements of dtype): xh N*(I+H), wcat (I+H)*H.  ws / ws_bytes:
  * optional scratch for the operator forward (gev2_gemm_fwd_desc.workspace).
  * One gather kernel and one operator forward per step.
+ * On a created (non-null) stream, when ws covers every step's operator scratch
+ * (gev2_gemm_fwd_workspace_size / gev2_gemm_bwd_workspace_size of one step),
+ * the step loop of a descriptor seen before is recorded into a HIP graph on
+ * its second call and replayed on later calls; the graph reads the buffers the
+ * descriptor names as they are at launch.  GEV2_RNN_GRAPH=0 disables this.
  */
 typedef struct gev2_rnn_desc {
   int32_t dtype;
