@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(256) grad_prep_kernel(PrepArgs p) {
 #pragma unroll
   for (int e = 0; e < EPC; ++e) sum[e] = 0.f;
   dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
-#pragma unroll 4
+#pragma unroll
     for (int r = rl; r < kPrepRows; r += 8) {
       const int m = r0 + r;
       if (!nok || m >= p.M) continue;
