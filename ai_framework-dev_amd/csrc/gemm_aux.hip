@@ -53,8 +53,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// PerM: one wave per row.
-template <typename T>
+// PerM: one wave per row.  VEC: rows are read in 16-byte chunks (every row and
+// slice start 16-byte aligned, N a multiple of the chunk).
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(256) bias_grad_rows_kernel(GradArgs p) {
   const int bz = blockIdx.y;
   const T* gY = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY;
@@ -63,11 +64,22 @@ __global__ void __launch_bounds__(256) bias_grad_rows_kernel(GradArgs p) {
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= p.M) return;
   float s = 0.f;
-  for (int n = lane; n < p.N; n += 64) {
-    const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
-    const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
-    s += g * act_grad(z, p.act, p.slope);
-  }
+  const T* grow = gY + (int64_t)m * p.ldgy;
+  const T* zrow = Z + (int64_t)m * p.ldz;
+  dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+    if constexpr (VEC) {
+      constexpr int EPC = Elem<T>::kPerChunk;
+      for (int n = lane * EPC; n < p.N; n += 64 * EPC) {
+        float gv[EPC], zv[EPC];
+        chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(grow + n), gv);
+        chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(zrow + n), zv);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) s += gv[e] * act_grad_t<ACT>(zv[e], p.slope);
+      }
+    } else {
+      for (int n = lane; n < p.N; n += 64) s += Elem<T>::load1(grow + n) * act_grad_t<ACT>(Elem<T>::load1(zrow + n), p.slope);
+    }
+  });
   s = wave_sum(s);
   if (lane == 0) p.gbias[(int64_t)bz * p.sGbias + m] = s;
 }
@@ -262,9 +274,15 @@ static hipError_t bias_grad_t(const GradArgs& a, int batch, hipStream_t s) {
     case kBiasPerN:
       hipLaunchKernelGGL(bias_grad_cols_kernel<T>, dim3((a.N + 63) / 64, batch), dim3(256), 0, s, a);
       break;
-    case kBiasPerM:
-      hipLaunchKernelGGL(bias_grad_rows_kernel<T>, dim3((a.M + 3) / 4, batch), dim3(256), 0, s, a);
+    case kBiasPerM: {
+      constexpr int EPC = Elem<T>::kPerChunk;
+      const auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+      const bool vec = al(a.gY) && al(a.Z) && a.N % EPC == 0 && a.ldgy % EPC == 0 && a.ldz % EPC == 0 &&
+                       (batch == 1 || (a.sgY % EPC == 0 && a.sZ % EPC == 0));
+      if (vec) hipLaunchKernelGGL((bias_grad_rows_kernel<T, true>), dim3((a.M + 3) / 4, batch), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((bias_grad_rows_kernel<T, false>), dim3((a.M + 3) / 4, batch), dim3(256), 0, s, a);
       break;
+    }
     case kBiasScalar:
       hipLaunchKernelGGL(bias_grad_all_kernel<T>, dim3(1, batch), dim3(256), 0, s, a);
       break;
