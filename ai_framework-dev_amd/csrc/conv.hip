@@ -210,6 +210,8 @@ __global__ void __launch_bounds__(256) acc_add_kernel(float* __restrict__ acc, c
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   float v = first ? 0.f : acc[i];
+  // the loads run ahead of the adds, which keep the slice order
+#pragma unroll 8
   for (int j = 0; j < slices; ++j) v += Elem<T>::load1(src + (int64_t)j * n + i);
   acc[i] = v;
 }
