@@ -1,6 +1,7 @@
 """CPU-side checks of the C-ABI library: it loads, exports every symbol that
 include/gev2_gemm.h declares, and its descriptor validation returns the
 reference's Status codes before any device work (no GPU needed)."""
+import ctypes
 import os
 import re
 
@@ -111,3 +112,26 @@ def test_forward_workspace_size(capi):
     assert _ws_size(capi, M=64) == 0                  # tile path
     assert _ws_size(capi, M=0) == 0
     assert _ws_size(capi, dtype=7) == -1
+
+
+def _bwd_ws(capi, **kw):
+    args = dict(dtype=2, M=64, N=256, K=128, A=1 << 20, B=1 << 24, gY=1 << 28, Z=1 << 30, gA=1 << 31,
+                gB=1 << 32, act="relu")
+    args.update(kw)
+    d = capi.bwd_desc(**args)
+    return capi.lib().gev2_gemm_bwd_workspace_size(ctypes.byref(d))
+
+
+def test_backward_workspace_size(capi):
+    """The backward's scratch: none when dY' is formed while loading (piecewise-linear act on a
+    problem under 2^30 multiply-adds); otherwise dY' (M*N elements, 256-byte rounded) plus, for a
+    PerN dBias on aligned rows, ceil(M/64)*N fp32 partials; -1 for a bad descriptor."""
+    assert _bwd_ws(capi) == 0                                          # relu, small: fused
+    assert _bwd_ws(capi, act="gelu") == 64 * 256 * 2                   # transcendental: materialised
+    big = dict(M=4096, N=4096, K=4096)
+    assert _bwd_ws(capi, **big) == 4096 * 4096 * 2                     # >= 2^30: materialised
+    assert _bwd_ws(capi, gBias=1 << 33, bias_kind=3, **big) == 4096 * 4096 * 2 + 64 * 4096 * 4
+    assert _bwd_ws(capi, gBias=1 << 33, bias_kind=3, gY=(1 << 28) + 2, **big) == 4096 * 4096 * 2  # unaligned: no partials
+    assert _bwd_ws(capi, act="tanh", M=3, N=10) == 256                 # rounded up to 256 bytes
+    assert _bwd_ws(capi, act="gelu", gA=0, gB=0) == 0                  # nothing to multiply
+    assert _bwd_ws(capi, dtype=7) == -1
