@@ -135,3 +135,11 @@ def test_backward_workspace_size(capi):
     assert _bwd_ws(capi, act="tanh", M=3, N=10) == 256                 # rounded up to 256 bytes
     assert _bwd_ws(capi, act="gelu", gA=0, gB=0) == 0                  # nothing to multiply
     assert _bwd_ws(capi, dtype=7) == -1
+
+
+def test_missing_library_fails_loudly(capi, monkeypatch, tmp_path):
+    """No CPU fallback: without libgev2.so the operator refuses to load."""
+    monkeypatch.setattr(capi, "_lib", None)
+    monkeypatch.setattr(capi, "LIB_PATH", str(tmp_path / "libgev2.so"))
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        capi.lib()
