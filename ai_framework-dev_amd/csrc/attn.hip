@@ -354,13 +354,15 @@ hipError_t launch_attn_fwd_qt(AttnArgs a, hipStream_t s) {
 // 32 queries per wave reuse each K / V fragment read twice; 16 per wave give
 // twice the waves.  The second is taken when the first would leave CUs with
 // fewer than two workgroups (one wave per SIMD cannot overlap the MFMA and
-// softmax phases of a block).
+// softmax phases of a block), and always at D = 128, where the 32-query
+// variant's registers allow only one wave per SIMD (measured: 140 against
+// 156 us at B 2, H 16, M = N = 2048).
 template <typename T, int D>
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
   const int64_t wg2 = (int64_t)a.BH * ((a.M + attn_wg_queries(2) - 1) / attn_wg_queries(2));
   const char* env = std::getenv("GEV2_ATTN_QT");        // 1 or 2 forces a variant (tuning runs)
   const int forced = env ? std::atoi(env) : 0;
-  if (forced == 2 || (forced != 1 && wg2 >= 512)) return launch_attn_fwd_qt<T, D, 2>(a, s);
+  if (forced == 2 || (forced != 1 && D == 64 && wg2 >= 512)) return launch_attn_fwd_qt<T, D, 2>(a, s);
   return launch_attn_fwd_qt<T, D, 1>(a, s);
 }
 

@@ -509,6 +509,9 @@ def main():
             ("c4_attn_f32", lambda: attn_cfg(ctx, capi.F32, 10, sets=2)),
             ("c4_attn_bwd_bf16", lambda: attn_bwd_cfg(ctx, capi.BF16, 20)),
             ("c4_attn_bwd_bf16_causal", lambda: attn_bwd_cfg(ctx, capi.BF16, 20, causal=True)),
+            ("attn_long_d128_bf16", lambda: attn_cfg(ctx, capi.BF16, 20, B=2, H=16, M=2048, N=2048, D=128, sets=2)),
+            ("attn_long_d128_bwd_bf16", lambda: attn_bwd_cfg(ctx, capi.BF16, 10, B=2, H=16, M=2048, N=2048, D=128)),
+            ("attn_long_d64_bf16", lambda: attn_cfg(ctx, capi.BF16, 20, B=2, H=32, M=2048, N=2048, D=64, sets=2)),
             ("c5a_conv_f32", lambda: conv_cfg(ctx, capi.F32, 20)),
             ("c5a_conv_bf16", lambda: conv_cfg(ctx, capi.BF16, 20)),
             ("c5a_conv2d_op_f32_per_image", lambda: conv_op_cfg(ctx, capi.F32, 5, 1)),
