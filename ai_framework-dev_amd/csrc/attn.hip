@@ -537,14 +537,19 @@ __device__ __forceinline__ void load_rows_c16swz(const i32x4_t& r, int64_t head_
   }
 }
 
-template <typename T, int D, bool MASKED>
-__global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
+// STAGES = 2 prefetches the next query block while this one is used; STAGES = 1
+// loads each block after the previous one is consumed and halves the LDS, so
+// more workgroups fit per CU.
+template <typename T, int D, bool MASKED, int STAGES>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(STAGES == 1 ? 3 : 1)))
+attn_bwd_kv_kernel(AttnBwdArgs ba) {
+  static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
   const AttnArgs& a = ba.f;
   constexpr int KS = D / 32, DT = D / 16, RB = D * 2, TILE = 64 * RB;
   constexpr int NL = 2 * (TILE / 1024 / 4);          // loads per wave per query block (Q and dO)
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES][2][TILE];
   // lse and Dq of a query block (first 256 bytes of each 1 KB load), wave 0's two extra loads
-  __shared__ __attribute__((aligned(1024))) float aux[2][2][256];
+  __shared__ __attribute__((aligned(1024))) float aux[STAGES][2][256];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -597,17 +602,27 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnBwdArgs ba) {
     if (wave == 0) load_aux(qb0 * 64, 0);
   }
   for (int qb = qb0; qb < nqb; ++qb) {
-    const int st = (qb - qb0) & 1;
-    if (qb + 1 < nqb) {
-      load_rows_b32swz<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
-      load_rows_b32swz<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
-      if (wave == 0) {
-        load_aux((qb + 1) * 64, st ^ 1);
-        __builtin_amdgcn_s_waitcnt(0x3f70 | ((NL + 2) & 0xf) | (((NL + 2) >> 4) << 14));
+    const int st = STAGES == 2 ? (qb - qb0) & 1 : 0;
+    if constexpr (STAGES == 2) {
+      if (qb + 1 < nqb) {
+        load_rows_b32swz<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
+        load_rows_b32swz<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
+        if (wave == 0) {
+          load_aux((qb + 1) * 64, st ^ 1);
+          __builtin_amdgcn_s_waitcnt(0x3f70 | ((NL + 2) & 0xf) | (((NL + 2) >> 4) << 14));
+        } else {
+          __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+        }
       } else {
-        __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt(0x3f70);
       }
     } else {
+      // the barrier that ended the previous block's use of stage 0 is behind us
+      if (qb > qb0) {
+        load_rows_b32swz<D>(rQ, qhead, qb * 64, a.M, wave, lane, q_lds(0));
+        load_rows_b32swz<D>(rO, qhead, qb * 64, a.M, wave, lane, o_lds(0));
+        if (wave == 0) load_aux(qb * 64, 0);
+      }
       __builtin_amdgcn_s_waitcnt(0x3f70);
     }
     __syncthreads();
@@ -805,8 +820,17 @@ hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
   const bool masked = a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f);
   if (ba.dK || ba.dV) {
     const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.N + 63) / 64)));
-    if (masked) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true>), grid, dim3(256), 0, s, ba);
-    else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false>), grid, dim3(256), 0, s, ba);
+    // one LDS stage at D = 128 (3 waves per SIMD instead of 2: 582 -> 574 us at B 2, H 16,
+    // M = N = 2048); at D = 64 both are equal (59.4 / 59.3 us at B 8, H 8, M = N = 512)
+    const char* env = std::getenv("GEV2_ATTN_KV_STAGES");   // 1 or 2 forces a variant (tuning runs)
+    const bool one = env ? std::atoi(env) == 1 : D == 128;
+    if (masked) {
+      if (one) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true, 1>), grid, dim3(256), 0, s, ba);
+      else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true, 2>), grid, dim3(256), 0, s, ba);
+    } else {
+      if (one) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false, 1>), grid, dim3(256), 0, s, ba);
+      else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false, 2>), grid, dim3(256), 0, s, ba);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
