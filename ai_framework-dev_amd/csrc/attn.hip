@@ -700,12 +700,15 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
   }
 }
 
-template <typename T, int D, bool MASKED>
-__global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnBwdArgs ba) {
+// STAGES as in attn_bwd_kv_kernel: 2 prefetches the next key block, 1 halves the LDS
+template <typename T, int D, bool MASKED, int STAGES>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(STAGES == 1 ? 3 : 1)))
+attn_bwd_q_kernel(AttnBwdArgs ba) {
+  static_assert(STAGES == 1 || STAGES == 2, "one or two LDS stages");
   const AttnArgs& a = ba.f;
   constexpr int KS = D / 32, DT = D / 16, RB = D * 2, TILE = 64 * RB;
   constexpr int NL = 2 * (TILE / 1024 / 4);
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][TILE];
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES][2][TILE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, col = lane & 15;
@@ -745,12 +748,21 @@ __global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnBwdArgs ba) {
   load_rows_b32swz<D>(rK, khead, 0, a.N, wave, lane, k_lds(0));
   load_rows_c16swz<D>(rV, khead, 0, a.N, wave, lane, v_lds(0));
   for (int kb = 0; kb < nkb; ++kb) {
-    const int st = kb & 1;
-    if (kb + 1 < nkb) {
-      load_rows_b32swz<D>(rK, khead, (kb + 1) * 64, a.N, wave, lane, k_lds(st ^ 1));
-      load_rows_c16swz<D>(rV, khead, (kb + 1) * 64, a.N, wave, lane, v_lds(st ^ 1));
-      __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+    const int st = STAGES == 2 ? kb & 1 : 0;
+    if constexpr (STAGES == 2) {
+      if (kb + 1 < nkb) {
+        load_rows_b32swz<D>(rK, khead, (kb + 1) * 64, a.N, wave, lane, k_lds(st ^ 1));
+        load_rows_c16swz<D>(rV, khead, (kb + 1) * 64, a.N, wave, lane, v_lds(st ^ 1));
+        __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x3f70);
+      }
     } else {
+      // the barrier that ended the previous block's use of stage 0 is behind us
+      if (kb > 0) {
+        load_rows_b32swz<D>(rK, khead, kb * 64, a.N, wave, lane, k_lds(0));
+        load_rows_c16swz<D>(rV, khead, kb * 64, a.N, wave, lane, v_lds(0));
+      }
       __builtin_amdgcn_s_waitcnt(0x3f70);
     }
     __syncthreads();
@@ -836,8 +848,17 @@ hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
   }
   if (ba.dQ) {
     const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.M + 63) / 64)));
-    if (masked) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true>), grid, dim3(256), 0, s, ba);
-    else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false>), grid, dim3(256), 0, s, ba);
+    // one LDS stage at D = 128 (4 waves per SIMD instead of 2: 559 -> 539 us at B 2, H 16,
+    // M = N = 2048); at D = 64 both are equal (60.1 / 60.4 us at B 8, H 8, M = N = 512)
+    const char* env = std::getenv("GEV2_ATTN_Q_STAGES");    // 1 or 2 forces a variant (tuning runs)
+    const bool one = env ? std::atoi(env) == 1 : D == 128;
+    if (masked) {
+      if (one) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true, 1>), grid, dim3(256), 0, s, ba);
+      else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true, 2>), grid, dim3(256), 0, s, ba);
+    } else {
+      if (one) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false, 1>), grid, dim3(256), 0, s, ba);
+      else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false, 2>), grid, dim3(256), 0, s, ba);
+    }
     e = hipGetLastError();
   }
   return e;
