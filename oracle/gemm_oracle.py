@@ -385,7 +385,7 @@ def conv2d_forward(X, W, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), act="
     for kh in range(Kh):
         for kw in range(Kw):
             win = _window(Xp, kh, kw, Ho, Wo, stride, dil)            # [N,C,Ho,Wo]
-            Z += np.einsum("nchw,oc->nohw", win, W[:, :, kh, kw])
+            Z += np.einsum("nchw,oc->nohw", win, W[:, :, kh, kw], optimize=True)
     if bias is not None:
         Z = Z + np.asarray(bias, np.float64).reshape(1, Cout, 1, 1)
     return act_forward(Z, act, slope), Z
@@ -408,10 +408,10 @@ def conv2d_backward(X, W, dY, Z, stride=(1, 1), pad=(0, 0), dil=(1, 1), act="non
     for kh in range(Kh):
         for kw in range(Kw):
             win = _window(Xp, kh, kw, Ho, Wo, stride, dil)
-            dW[:, :, kh, kw] = np.einsum("nohw,nchw->oc", dZ, win)
+            dW[:, :, kh, kw] = np.einsum("nohw,nchw->oc", dZ, win, optimize=True)
             h0, w0 = kh * dil[0], kw * dil[1]
             dXp[:, :, h0:h0 + stride[0] * (Ho - 1) + 1:stride[0], w0:w0 + stride[1] * (Wo - 1) + 1:stride[1]] += \
-                np.einsum("nohw,oc->nchw", dZ, W[:, :, kh, kw])
+                np.einsum("nohw,oc->nchw", dZ, W[:, :, kh, kw], optimize=True)
     dX = dXp[:, :, pad[0]:pad[0] + H, pad[1]:pad[1] + Wd]
     return {"dZ": dZ, "dW": dW, "dB": dZ.sum(axis=(0, 2, 3)), "dX": dX}
 
@@ -465,7 +465,7 @@ def _sdpa_scores(Q, K, scale, causal, mask, mask_kind):
     masked entry is formed as the reference forms it, by an fp32 addition of -1e9 (or of the
     F32 mask value) to the fp32-rounded score; unmasked entries stay float64."""
     Q, K = np.asarray(Q, np.float64), np.asarray(K, np.float64)
-    S = np.einsum("bhmd,bhnd->bhmn", Q, K) * scale
+    S = np.einsum("bhmd,bhnd->bhmn", Q, K, optimize=True) * scale
     M, N = S.shape[2], S.shape[3]
     add = np.zeros(S.shape, np.float32)
     hit = np.zeros(S.shape, bool)
@@ -501,7 +501,7 @@ def sdpa_forward(Q, K, V, scale: float = 0.0, causal: bool = False, mask=None, m
     E = np.exp(S - mx)
     l = E.sum(axis=-1, keepdims=True)
     P = E / l
-    Y = np.einsum("bhmn,bhnd->bhmd", P, np.asarray(V, np.float64))
+    Y = np.einsum("bhmn,bhnd->bhmd", P, np.asarray(V, np.float64), optimize=True)
     return Y, P, (mx + np.log(l))[..., 0]
 
 
@@ -512,10 +512,10 @@ def sdpa_backward(Q, K, V, dY, scale: float = 0.0, causal: bool = False, mask=No
     sc = scale if scale != 0.0 else 1.0 / math.sqrt(D)
     _, P, _ = sdpa_forward(Q, K, V, scale, causal, mask, mask_kind)
     _, hit = _sdpa_scores(Q, K, sc, causal, mask, mask_kind)
-    dV = np.einsum("bhmn,bhmd->bhnd", P, dY)
-    dP = np.einsum("bhmd,bhnd->bhmn", dY, V)
+    dV = np.einsum("bhmn,bhmd->bhnd", P, dY, optimize=True)
+    dP = np.einsum("bhmd,bhnd->bhmn", dY, V, optimize=True)
     dS = P * (dP - (dP * P).sum(axis=-1, keepdims=True))
     dS = np.where(hit, 0.0, dS)
-    dQ = sc * np.einsum("bhmn,bhnd->bhmd", dS, K)
-    dK = sc * np.einsum("bhmn,bhmd->bhnd", dS, Q)
+    dQ = sc * np.einsum("bhmn,bhnd->bhmd", dS, K, optimize=True)
+    dK = sc * np.einsum("bhmn,bhmd->bhnd", dS, Q, optimize=True)
     return {"dQ": dQ, "dK": dK, "dV": dV}

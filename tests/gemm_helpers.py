@@ -11,6 +11,9 @@ DT_NAMES = {F32: "f32", F16: "f16", BF16: "bf16"}
 # unit roundoff of the output storage type (one RNE rounding)
 U_OUT = {F32: 2.0 ** -24, F16: 2.0 ** -11, BF16: 2.0 ** -8}
 U_ACC = 2.0 ** -24   # fp32 accumulation
+# absolute error of one RNE rounding in the subnormal range: half the subnormal spacing
+# (fp16 2^-24, bf16 2^-133, fp32 2^-149), where the relative bound u*|x| no longer holds
+TINY_OUT = {F32: 2.0 ** -150, F16: 2.0 ** -25, BF16: 2.0 ** -134}
 
 
 def rng(seed: int) -> np.random.Generator:

@@ -75,6 +75,7 @@ FUSED_CASES = [
     (1, 2, 96, 160, 64, False, O.MASK_F32),
     (1, 1, 1, 1, 64, False, O.MASK_NONE),          # one query, one key: Y = V
     (1, 2, 3, 200, 128, True, O.MASK_NONE),        # M < N with causal
+    (8, 8, 512, 512, 64, False, O.MASK_NONE),      # the C4 shape (8 sequences x 8 heads)
 ]
 
 
@@ -153,6 +154,7 @@ BWD_CASES = [
     (1, 2, 64, 80, 64, False, O.MASK_F32),
     (1, 1, 1, 1, 64, False, O.MASK_NONE),
     (1, 1, 5, 130, 64, True, O.MASK_NONE),
+    (8, 8, 512, 512, 64, False, O.MASK_NONE),      # the C4 shape
 ]
 
 
