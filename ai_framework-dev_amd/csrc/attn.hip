@@ -360,9 +360,7 @@ hipError_t launch_attn_fwd_qt(AttnArgs a, hipStream_t s) {
 template <typename T, int D>
 hipError_t launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
   const int64_t wg2 = (int64_t)a.BH * ((a.M + attn_wg_queries(2) - 1) / attn_wg_queries(2));
-  const char* env = std::getenv("GEV2_ATTN_QT");        // 1 or 2 forces a variant (tuning runs)
-  const int forced = env ? std::atoi(env) : 0;
-  if (forced == 2 || (forced != 1 && D == 64 && wg2 >= 512)) return launch_attn_fwd_qt<T, D, 2>(a, s);
+  if (D == 64 && wg2 >= 512) return launch_attn_fwd_qt<T, D, 2>(a, s);
   return launch_attn_fwd_qt<T, D, 1>(a, s);
 }
 
@@ -834,14 +832,11 @@ hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.N + 63) / 64)));
     // one LDS stage at D = 128 (3 waves per SIMD instead of 2: 582 -> 574 us at B 2, H 16,
     // M = N = 2048); at D = 64 both are equal (59.4 / 59.3 us at B 8, H 8, M = N = 512)
-    const char* env = std::getenv("GEV2_ATTN_KV_STAGES");   // 1 or 2 forces a variant (tuning runs)
-    const bool one = env ? std::atoi(env) == 1 : D == 128;
+    constexpr bool one = D == 128;
     if (masked) {
-      if (one) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true, 1>), grid, dim3(256), 0, s, ba);
-      else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true, 2>), grid, dim3(256), 0, s, ba);
+      hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, true, one ? 1 : 2>), grid, dim3(256), 0, s, ba);
     } else {
-      if (one) hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false, 1>), grid, dim3(256), 0, s, ba);
-      else hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false, 2>), grid, dim3(256), 0, s, ba);
+      hipLaunchKernelGGL((attn_bwd_kv_kernel<T, D, false, one ? 1 : 2>), grid, dim3(256), 0, s, ba);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -850,14 +845,11 @@ hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.M + 63) / 64)));
     // one LDS stage at D = 128 (4 waves per SIMD instead of 2: 559 -> 539 us at B 2, H 16,
     // M = N = 2048); at D = 64 both are equal (60.1 / 60.4 us at B 8, H 8, M = N = 512)
-    const char* env = std::getenv("GEV2_ATTN_Q_STAGES");    // 1 or 2 forces a variant (tuning runs)
-    const bool one = env ? std::atoi(env) == 1 : D == 128;
+    constexpr bool one = D == 128;
     if (masked) {
-      if (one) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true, 1>), grid, dim3(256), 0, s, ba);
-      else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true, 2>), grid, dim3(256), 0, s, ba);
+      hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, true, one ? 1 : 2>), grid, dim3(256), 0, s, ba);
     } else {
-      if (one) hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false, 1>), grid, dim3(256), 0, s, ba);
-      else hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false, 2>), grid, dim3(256), 0, s, ba);
+      hipLaunchKernelGGL((attn_bwd_q_kernel<T, D, false, one ? 1 : 2>), grid, dim3(256), 0, s, ba);
     }
     e = hipGetLastError();
   }

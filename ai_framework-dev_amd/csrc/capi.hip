@@ -11,6 +11,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/gev2_gemm.h"
 #include "gev2_kernels.hpp"
@@ -43,6 +44,11 @@ namespace {
 
 thread_local std::string t_last_error;
 thread_local const char* t_last_path = "";
+// captures this thread has open (gev2_graph_begin .. gev2_graph_end), and the
+// device frees requested meanwhile (a free during capture would invalidate it;
+// e.g. a Python array whose last reference goes away inside the capture block)
+thread_local int t_captures = 0;
+thread_local std::vector<void*> t_deferred_frees;
 
 int fail(int status, const std::string& msg) {
   t_last_error = msg;
@@ -155,13 +161,34 @@ const char* cfg_name(int cfg, bool vec, bool dl = false) {
 
 std::mutex g_ws_mu;
 
+// True while `s` is being recorded into a HIP graph.  A stream whose capture
+// state cannot be read (the null stream while another thread captures in
+// global mode) counts as capturing.
+bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
+
+bool aligned256(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 255u) == 0; }
+
 // Scratch for the forward's split-K partial sums and the backward's dY' when
 // the caller passes no workspace: one buffer per (device, stream), grown on
 // demand (a stream runs its calls in order, so they can share it).  hipFree
 // waits for queued work that may still read the old buffer.
+// It is never used while the stream is being captured: the operator then
+// takes a path that needs no scratch (or the caller's workspace), so no graph
+// ever refers to one of these buffers and growing one cannot leave a graph
+// pointing at freed memory.
 std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_stream_ws;
 
 int get_stream_ws(hipStream_t s, size_t bytes, void** out) {
+  if (stream_capturing(s))
+    return fail(GEV2_MISSING_INPUT, "the stream is being captured into a graph and no workspace of " +
+                                        std::to_string(bytes) + " bytes was passed (nothing is allocated during capture)");
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -291,9 +318,12 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   if (pl.skinny) {
     float* part = nullptr;
     if (pl.ws_bytes > 0) {
-      if (d->workspace && d->workspace_bytes >= pl.ws_bytes &&
-          (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
+      if (aligned256(d->workspace) && d->workspace_bytes >= pl.ws_bytes) {
         part = static_cast<float*>(d->workspace);
+      } else if (stream_capturing(s)) {
+        // no workspace under capture: the dot-product kernel, which needs none
+        pl.sk.x_vec = std::min(pl.sk.x_vec, 1);
+        pl.split = false;
       } else {
         void* w = nullptr;
         st = get_stream_ws(s, static_cast<size_t>(pl.ws_bytes), &w);
@@ -338,14 +368,28 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
 
 namespace {
 
-// Whether the backward materialises dY' = dY (.) act'(Z), and the scratch it
-// then needs: dY' (batch*M*N elements, 256-byte rounded) plus the PerN dBias
-// partials.  Shared by gev2_gemm_bwd and gev2_gemm_bwd_workspace_size.
+// Whether the backward materialises dY' = dY (.) act'(Z), the scratch it then
+// needs, and where the PerN dBias partials of that pass go.  Shared by
+// gev2_gemm_bwd and gev2_gemm_bwd_workspace_size.
+//
+// The partials (batch x row blocks x N fp32) are parked in an output that is
+// written only afterwards: the dX output when it is a dense array (ld = K,
+// slices back to back) large enough, else the dW output on the same terms,
+// else after dY' in the workspace.  The workspace therefore needs no more than
+// dY' itself (batch*M*N elements) in the usual case, which is never more than
+// the M*N fp32 dZ buffer the reference's capture-safe backward passes.
+enum PartHome { kPartNone = 0, kPartWorkspace = 1, kPartDx = 2, kPartDw = 3 };
+
 struct BwdScratch {
   bool materialise{false}, prep_vec{false}, sums{false};
   int row_blocks{0};
-  int64_t gz_bytes{0}, need{0};
+  int part_home{kPartNone};
+  int64_t gz_bytes{0};     // dY': batch*M*N elements
+  int64_t part_bytes{0};   // dBias partials (sums only)
+  int64_t need{0};         // what gev2_gemm_bwd_workspace_size reports
 };
+
+int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
 
 BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
   BwdScratch r;
@@ -364,8 +408,23 @@ BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
                vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt);
   r.sums = r.prep_vec && want_bias && d->bias_kind == GEV2_BIAS_PER_N;
   r.row_blocks = static_cast<int>((M + gev2::kPrepRows - 1) / gev2::kPrepRows);
-  r.gz_bytes = ((static_cast<int64_t>(batch) * M * N * es + 255) / 256) * 256;
-  r.need = r.gz_bytes + (r.sums ? static_cast<int64_t>(batch) * r.row_blocks * N * 4 : 0);
+  r.gz_bytes = static_cast<int64_t>(batch) * M * N * es;
+  r.need = r.gz_bytes;
+  if (!r.sums) return r;
+  r.part_bytes = static_cast<int64_t>(batch) * r.row_blocks * N * 4;
+  const auto dense_home = [&](const void* p, int64_t ld, int64_t stride, int64_t rows, int64_t cols) {
+    if (!p || (reinterpret_cast<uintptr_t>(p) & 15u) != 0) return false;
+    if (dense_ld(ld, cols) != cols || (batch > 1 && stride != rows * cols)) return false;
+    return static_cast<int64_t>(batch) * rows * cols * es >= r.part_bytes;
+  };
+  if (dense_home(d->gA, d->ldga, d->stride_ga, M, K)) {
+    r.part_home = kPartDx;
+  } else if (dense_home(d->gB, d->ldgb, d->stride_gb, K, N)) {
+    r.part_home = kPartDw;
+  } else {
+    r.part_home = kPartWorkspace;
+    r.need = round256(r.gz_bytes) + r.part_bytes;
+  }
   return r;
 }
 
@@ -416,19 +475,37 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   bool fused = true;
   bool bias_done = false;
   const BwdScratch sc = bwd_scratch(d);
+  // Where dY' goes: the caller's workspace when it holds dY'; otherwise the
+  // per-stream buffer, except under graph capture, where the GEMMs apply act'
+  // to dY on load instead for none / ReLU / LeakyReLU, and the transcendental
+  // activations are refused (nothing is allocated during capture).
+  void* ws = nullptr;
+  bool sums = sc.sums;
   if (sc.materialise) {
-    const bool prep_vec = sc.prep_vec, sums = sc.sums;
-    const int row_blocks = sc.row_blocks;
-    const int64_t gz_bytes = sc.gz_bytes;
-    const int64_t need = sc.need;
-    void* ws = nullptr;
-    if (d->workspace && d->workspace_bytes >= need && (reinterpret_cast<uintptr_t>(d->workspace) & 255) == 0) {
+    if (aligned256(d->workspace) && d->workspace_bytes >= sc.gz_bytes) {
       ws = d->workspace;
-    } else {
-      st = get_stream_ws(s, static_cast<size_t>(need), &ws);
+      // partials parked after dY' need the larger size; without it dBias
+      // falls back to the column-sum kernel below
+      if (sums && sc.part_home == kPartWorkspace && d->workspace_bytes < sc.need) sums = false;
+    } else if (!stream_capturing(s)) {
+      st = get_stream_ws(s, static_cast<size_t>(sc.need), &ws);
       if (st != GEV2_OK) return st;
+    } else if (!linear) {
+      // act' is applied on load for the piecewise-linear activations only
+      return fail(GEV2_MISSING_INPUT, "the stream is being captured into a graph: a GELU / Sigmoid / Tanh backward "
+                                      "needs a dY' workspace of " + std::to_string(sc.gz_bytes) +
+                                      " bytes (nothing is allocated during capture)");
     }
-    float* partial = sums ? reinterpret_cast<float*>(static_cast<char*>(ws) + gz_bytes) : nullptr;
+  }
+  if (ws) {
+    const bool prep_vec = sc.prep_vec;
+    const int row_blocks = sc.row_blocks;
+    float* partial = nullptr;
+    if (sums) {
+      partial = sc.part_home == kPartDx   ? static_cast<float*>(d->gA)
+                : sc.part_home == kPartDw ? static_cast<float*>(d->gB)
+                                          : reinterpret_cast<float*>(static_cast<char*>(ws) + round256(sc.gz_bytes));
+    }
     hipError_t e;
     if (prep_vec) {
       gev2::PrepArgs pa{};
@@ -586,6 +663,12 @@ int gev2_malloc(void** ptr, size_t bytes) {
   return GEV2_OK;
 }
 int gev2_free(void* ptr) {
+  if (t_captures > 0) {
+    // hipFree is not allowed while this thread captures (it would invalidate
+    // the graph): release the memory when the capture ends
+    t_deferred_frees.push_back(ptr);
+    return GEV2_OK;
+  }
   GEV2_HIP_CALL(hipFree(ptr), "hipFree");
   return GEV2_OK;
 }
@@ -663,19 +746,29 @@ int gev2_event_elapsed_ms(float* ms, void* start, void* stop) {
 }
 
 // HIP graph capture of a stream's work (thread-local capture mode: other
-// threads' HIP calls are unaffected).  Capture is valid only for work that
-// allocates nothing: pass every workspace, or make one call outside the
-// capture first so that the per-stream buffer already exists.
+// threads' HIP calls are unaffected).  The operator calls allocate nothing
+// while their stream is capturing (get_stream_ws refuses; the forward and
+// backward take their scratch-free paths instead).
 int gev2_graph_begin(void* stream) {
   if (!stream) return fail(GEV2_INVALID_ARGUMENT, "capture needs a created stream, not the null stream");
   GEV2_HIP_CALL(hipStreamBeginCapture(reinterpret_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
                 "hipStreamBeginCapture");
+  ++t_captures;
   return GEV2_OK;
 }
 int gev2_graph_end(void* stream, void** exec) {
   if (!exec) return fail(GEV2_INVALID_ARGUMENT, "exec is null");
   hipGraph_t g = nullptr;
-  GEV2_HIP_CALL(hipStreamEndCapture(reinterpret_cast<hipStream_t>(stream), &g), "hipStreamEndCapture");
+  const hipError_t ec = hipStreamEndCapture(reinterpret_cast<hipStream_t>(stream), &g);
+  if (t_captures > 0 && --t_captures == 0) {
+    // the frees asked for during the capture
+    for (void* p : t_deferred_frees) (void)hipFree(p);
+    t_deferred_frees.clear();
+  }
+  if (ec != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return hip_fail(ec, "hipStreamEndCapture");
+  }
   hipGraphExec_t e = nullptr;
   const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);

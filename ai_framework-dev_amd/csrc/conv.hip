@@ -394,15 +394,27 @@ int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* d, void* stream) {
     if (!d->gw || !d->acc_w) return conv_fail(GEV2_MISSING_INPUT, "dW needs the gw and acc_w workspaces");
     fit(d->gw_bytes, CK * es);
   }
+  // dB: acc_b holds the running sum [Cout] and, when it has room, the chunk's
+  // per-image slices [chunk][Cout].  With room for the sum only (the
+  // reference's gy_rows is Cout*Ho*Wo floats, so Cout floats at a 1x1 output),
+  // each image's slice goes to dB itself, one image per call: dB is written
+  // from the sum only after the last image.
+  bool db_slices_in_acc = true;
   if (d->dB) {
-    if (!d->acc_b) return conv_fail(GEV2_MISSING_INPUT, "dB needs the acc_b workspace");
-    fit(d->acc_b_bytes - 4 * (int64_t)d->Cout, 4 * (int64_t)d->Cout);
+    if (!d->acc_b || d->acc_b_bytes < 4 * (int64_t)d->Cout)
+      return conv_fail(GEV2_MISSING_INPUT, "dB needs the acc_b workspace (at least Cout floats)");
+    if (d->acc_b_bytes >= 8 * (int64_t)d->Cout) {
+      fit(d->acc_b_bytes - 4 * (int64_t)d->Cout, 4 * (int64_t)d->Cout);
+    } else {
+      db_slices_in_acc = false;
+      chunk = std::min<int64_t>(chunk, 1);
+    }
   }
   if (chunk < 1) return conv_fail(GEV2_MISSING_INPUT, "a workspace is smaller than one image needs");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   float* accW = d->acc_w;               // [Cout*K] sum of dW_n
   float* accB = d->acc_b;               // [Cout]   sum of dB_n
-  float* gb = d->acc_b + d->Cout;       // [chunk][Cout] dB_n
+  float* gb = db_slices_in_acc ? d->acc_b + d->Cout : d->dB;   // [chunk][Cout] dB_n
   for (int64_t n0 = 0; n0 < d->N; n0 += chunk) {
     const int c = static_cast<int>(std::min<int64_t>(chunk, d->N - n0));
     const char* x = static_cast<const char*>(d->X) + n0 * d->Cin * d->H * d->W * es;

@@ -1,5 +1,7 @@
 // Small backward helpers for the cases the fused MFMA passes do not cover:
-//   - gC = beta * gY (.) act'(Z)          (regemm_backward.cu:116-118)
+//   - gC = beta * gY (.) act'(Z), and gC = 0 when beta = 0 (the reference
+//     zero-fills gC when C is absent or beta = 0: regemm_backward.cu:115-117,
+//     :183-189)
 //   - bias gradient when it cannot ride the dW pass: PerM (row sums), Scalar,
 //     or PerN without a dW output.  (regemm_backward.cu:120-129 accumulates
 //     these with fp32 atomics; here every sum has a fixed order.)
@@ -18,6 +20,11 @@ __global__ void __launch_bounds__(256) grad_elementwise_kernel(GradArgs p) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int m = static_cast<int>(i / p.N), n = static_cast<int>(i - (int64_t)m * p.N);
+    if (p.beta == 0.f) {
+      // beta = 0: gC is zero, whatever dY holds (no 0 * inf)
+      Elem<T>::store1(out + (int64_t)m * p.ldout + n, 0.f);
+      continue;
+    }
     const float g = Elem<T>::load1(gY + (int64_t)m * p.ldgy + n);
     const float z = Elem<T>::load1(Z + (int64_t)m * p.ldz + n);
     Elem<T>::store1(out + (int64_t)m * p.ldout + n, p.beta * (g * act_grad(z, p.act, p.slope)));

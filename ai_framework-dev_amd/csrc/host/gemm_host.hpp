@@ -5,7 +5,9 @@
 // gemm/launcher.cu:147-383), so its C++ callers (conv2d/launcher.cu:216,429,
 // rnn/launcher.cu:194,345) and the pybind module bind unchanged.  The
 // implementation validates the views and forwards to the C ABI of
-// libgev2.so (include/gev2_gemm.h); it never allocates device memory.
+// libgev2.so (include/gev2_gemm.h).  It allocates nothing itself; the
+// operator allocates scratch only when the caller's workspace is missing or
+// too small, and never while the stream is being captured into a graph.
 //
 // Differences a caller can observe:
 //   - F16 and BF16 tensors are accepted (all of A, B, Y, Z, gY, gA, gB, gC in
@@ -48,9 +50,10 @@ Status GemmCudaBackward(const Tensor& A, const Tensor& B, const Tensor* C, const
                         const GemmAttrs& attrs, StreamHandle stream,
                         const GemmWorkspace* ws = nullptr);
 
-// Capture-safe form (gemm/api.hpp:162-186): the dZ buffer and cuBLASLt
-// workspace of the reference are accepted for interface compatibility; this
-// build allocates nothing in either form, so the two are equivalent.
+// Capture-safe form (gemm/api.hpp:166-188): the dZ buffer (M*N fp32) is the
+// operator's dY' workspace, which always suffices (dY' takes M*N elements and
+// the dBias partials are parked in the gA or gB output), so the call never
+// allocates.  The cuBLASLt workspace is validated and otherwise unused.
 inline Status GemmCudaBackwardInto(const Tensor& A, const Tensor& B, const Tensor* C,
                                    const Tensor& gY, const Tensor& Z, Tensor* gA, Tensor* gB,
                                    Tensor* gC, Tensor* gBias, const GemmAttrs& attrs,

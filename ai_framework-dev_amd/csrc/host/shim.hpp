@@ -111,8 +111,10 @@ struct GemmAttrs {
   float beta{0.0f};    // unused, as in the reference
 };
 
-// The backward of this build never needs scratch; the fields are accepted and
-// validated like the reference's (alignment of lt_workspace, size of scratch).
+// Workspaces of a call (gemm/api.hpp:97-104), validated like the reference's
+// (alignment of lt_workspace, size of scratch).  `scratch` is the operator's
+// workspace: the backward's dY' (M*N elements suffice) and, in the forward,
+// the split-K partials of skinny 16-bit problems; lt_workspace is unused.
 struct alignas(256) GemmWorkspace {
   void* lt_workspace = nullptr;
   std::size_t lt_workspace_bytes = 0;

@@ -314,7 +314,9 @@ int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
     f.A = d->xh; f.lda = IH; f.B = d->wcat; f.ldb = d->H; f.bias = d->bias;
     f.Y = d->Y; f.ldy = (int64_t)d->T * d->H;
     const int64_t need = gev2_gemm_fwd_workspace_size(&f);
-    graph_ok = need == 0 || (need > 0 && d->ws && d->ws_bytes >= need);
+    // the operator takes the caller's workspace only when it is 256-byte aligned
+    graph_ok = need == 0 || (need > 0 && d->ws && d->ws_bytes >= need &&
+                             (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0);
   }
   return run_cached(d, 'f', s, graph_ok, [&]() -> int {
   int st = GEV2_OK;

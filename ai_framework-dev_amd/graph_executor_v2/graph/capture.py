@@ -7,10 +7,11 @@ recorder uses with CuPy (python/graph_executor_v2/graph/graph_exec.py:119-136):
     gexec = cap.graph.instantiate()
     gexec.launch(stream)
 
-The calls inside the block are recorded, not run.  They must allocate nothing:
-the *_into paths take every buffer from the caller, and the operator's own
-per-stream buffer (skinny forwards, a materialised dY') must already exist,
-which one eager call on the same stream before the capture guarantees.
+The calls inside the block are recorded, not run, and allocate nothing: the
+*_into paths take every buffer from the caller (the dZ buffer is the
+operator's dY' workspace), and an operator call that lacks a workspace it
+would use eagerly takes its scratch-free kernels while the stream captures.
+No eager warm-up call is needed.
 """
 from __future__ import annotations
 

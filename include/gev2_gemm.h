@@ -5,12 +5,12 @@
  * This is the thin C layer that the C++ host code behind the Python binding
  * (graph_executor_v2.ops._ops_gemm) calls.  It replaces, one for one:
  *   gev2_gemm_fwd  <- ai::cuda::shim::GemmCudaLaunch
- *                     (graph_executor_v2/backends/cuda/ops/gemm/api.hpp:509-518,
+ *                     (graph_executor_v2/backends/cuda/ops/gemm/api.hpp:124-134,
  *                      launcher.cu:147-274) and, with batch > 1 or a transpose,
  *                     the per-slice GEMM loops of conv2d/launcher.cu:180-227 and
  *                     sdpa/launcher.cu:185-270
  *   gev2_gemm_bwd  <- ai::cuda::shim::GemmCudaBackward / GemmCudaBackwardInto
- *                     (gemm/api.hpp:535-573, launcher.cu:279-383,
+ *                     (gemm/api.hpp:150-163, 166-188, launcher.cu:279-383,
  *                      kernels/regemm_backward.cu:151-301)
  * Its descriptor style (one POD of pointers, sizes and enums per call) follows
  * the reference's earlier C ABI, dev/backend/graph_executor_v2/include/
@@ -29,6 +29,12 @@
  *     16-bit problems (gev2_gemm_fwd_workspace_size gives the size, 0 for all
  *     other problems) and the backward's materialised dY'.  Such a buffer is
  *     allocated once per (device, stream) and kept until gev2_stream_destroy.
+ *   - Nothing is allocated while `stream` is being captured into a HIP graph,
+ *     so a captured graph never refers to library-owned memory.  Without a
+ *     large enough workspace the forward then uses its scratch-free skinny
+ *     kernel, and the backward applies act' to dY as its GEMMs load it (none /
+ *     ReLU / LeakyReLU) or, for GELU / Sigmoid / Tanh, which need dY' in a
+ *     workspace, returns GEV2_MISSING_INPUT.
  */
 #ifndef GEV2_GEMM_H_
 #define GEV2_GEMM_H_
@@ -79,8 +85,9 @@ enum { GEV2_BIAS_NONE = 0, GEV2_BIAS_SCALAR = 1, GEV2_BIAS_PER_M = 2, GEV2_BIAS_
  * alpha = 1 and no transposes (it returns TransposeNotSupported for them).
  * workspace: optional scratch (256-byte aligned) of at least
  * gev2_gemm_fwd_workspace_size(desc) bytes; NULL or too small makes the
- * library use its own per-(device, stream) buffer.  Plays the role of the
- * reference's GemmWorkspace (gemm/api.hpp:97-104, GemmCudaLaunch's ws).
+ * library use its own per-(device, stream) buffer (outside graph capture).
+ * Plays the role of the reference's GemmWorkspace (gemm/api.hpp:97-104,
+ * GemmCudaLaunch's ws).
  */
 typedef struct gev2_gemm_fwd_desc {
   int32_t dtype;
@@ -130,13 +137,18 @@ typedef struct gev2_gemm_bwd_desc {
   void* gC;       int64_t ldgc, stride_gc;
   float* gBias;   int64_t stride_gbias;
   /* Optional scratch (256-byte aligned) for dY' = dY (.) act'(Z): batch*M*N
-   * elements of dtype, rounded up to 256 bytes, plus batch*ceil(M/64)*N floats
-   * of dBias partial sums when a PerN gBias is requested.  Used when gZ is
-   * materialised: always for GELU / Sigmoid / Tanh, and for large problems
-   * (M*N*K*batch >= 2^30).  NULL or too small: the library uses a buffer it
-   * allocates once per (device, stream) and keeps (make that first call outside
-   * HIP-graph capture).  Plays the role of the reference's
-   * GemmWorkspace::scratch (gemm/api.hpp:97-104). */
+   * elements of dtype.  Used when gZ is materialised: always for GELU /
+   * Sigmoid / Tanh, and for large problems (M*N*K*batch >= 2^30).  A PerN
+   * dBias is summed by the same pass into batch*ceil(M/64)*N float partials,
+   * parked in the gA output when gA is dense (ldga = K, slices back to back)
+   * and large enough, else in a dense gB, else after dY' in this workspace
+   * (then rounded up to 256 bytes; gev2_gemm_bwd_workspace_size includes
+   * them).  So the reference's M*N fp32 dZ scratch always holds what is
+   * needed.  NULL or too small for dY': the library uses a buffer it
+   * allocates once per (device, stream) and keeps, or, while the stream is
+   * being captured, forms dY' while loading instead (none / ReLU / LeakyReLU;
+   * other activations return GEV2_MISSING_INPUT then).  Plays the role of the
+   * reference's GemmWorkspace::scratch (gemm/api.hpp:97-104). */
   void* workspace; int64_t workspace_bytes;
 } gev2_gemm_bwd_desc;
 
@@ -147,8 +159,10 @@ int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* desc);
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* desc, void* stream);
 /* Scratch bytes gev2_gemm_bwd uses for `desc` (0: none, dY' is formed while
  * loading); -1 for an invalid descriptor.  A `workspace` this large (256-byte
- * aligned) keeps the call off the per-stream buffer.  No counterpart in the
- * reference (its scratch is GemmWorkspace::scratch, sized by the caller). */
+ * aligned) keeps the call off the per-stream buffer; one of batch*M*N
+ * elements does too, with dBias then summed by a separate column pass when
+ * its partials had no other home.  No counterpart in the reference (its
+ * scratch is GemmWorkspace::scratch, sized by the caller). */
 int64_t gev2_gemm_bwd_workspace_size(const gev2_gemm_bwd_desc* desc);
 
 /*
@@ -392,6 +406,8 @@ int gev2_get_device(int* device);
 /* name (NUL-terminated, truncated to name_len), compute units, peak clock kHz */
 int gev2_device_info(int device, char* name, size_t name_len, int* cu_count, int* clock_khz);
 int gev2_malloc(void** ptr, size_t bytes);
+/* A free requested while this thread has a capture open (gev2_graph_begin ..
+ * gev2_graph_end) is carried out when the capture ends. */
 int gev2_free(void* ptr);
 int gev2_memcpy_htod(void* dst, const void* src, size_t bytes);
 int gev2_memcpy_dtoh(void* dst, const void* src, size_t bytes);
@@ -411,9 +427,10 @@ int gev2_event_elapsed_ms(float* ms, void* start, void* stop);
  * HIP graph capture of a stream's work: begin, run the calls to record on
  * `stream`, end (instantiates; *exec receives the executable graph), then
  * launch it any number of times and destroy it.  Replaces the CuPy graph
- * capture of the reference's Python layer (graph/graph_exec.py:119-136).  Only
- * work that allocates nothing may be captured: pass every workspace, or make
- * one call outside the capture first (the per-stream buffer then exists).
+ * capture of the reference's Python layer (graph/graph_exec.py:119-136).  The
+ * GEMM calls allocate nothing under capture (see Conventions), so they may be
+ * recorded without a warm-up call; with every workspace passed, the recorded
+ * kernels are the same as the eager ones.
  */
 int gev2_graph_begin(void* stream);
 int gev2_graph_end(void* stream, void** exec);

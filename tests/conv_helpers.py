@@ -12,6 +12,9 @@ GEOMS = {
     "stride2": dict(N=2, Cin=5, H=11, W=9, Cout=12, Kh=3, Kw=2, stride=(2, 1), pad=(0, 2), dil=(1, 1)),
     "dilated": dict(N=2, Cin=4, H=9, W=10, Cout=8, Kh=2, Kw=3, stride=(1, 2), pad=(1, 0), dil=(2, 1)),
     "pointwise": dict(N=2, Cin=6, H=5, W=7, Cout=4, Kh=1, Kw=1, stride=(1, 1), pad=(0, 0), dil=(1, 1)),
+    # kernel the size of the input: a 1x1 output, so the reference-sized gy_rows workspace
+    # (Cout*Ho*Wo floats) holds only the dB sum
+    "1x1-output": dict(N=3, Cin=4, H=3, W=5, Cout=6, Kh=3, Kw=5, stride=(1, 1), pad=(0, 0), dil=(1, 1)),
 }
 
 

@@ -124,17 +124,37 @@ def _bwd_ws(capi, **kw):
 
 def test_backward_workspace_size(capi):
     """The backward's scratch: none when dY' is formed while loading (piecewise-linear act on a
-    problem under 2^30 multiply-adds); otherwise dY' (M*N elements, 256-byte rounded) plus, for a
-    PerN dBias on aligned rows, ceil(M/64)*N fp32 partials; -1 for a bad descriptor."""
+    problem under 2^30 multiply-adds); otherwise dY' (batch*M*N elements).  A PerN dBias on
+    aligned rows is summed into ceil(M/64)*N fp32 partials parked in the dX output when it is
+    dense and large enough, else in a dense dW output, else after dY' (256-byte rounded) in the
+    workspace; -1 for a bad descriptor."""
     assert _bwd_ws(capi) == 0                                          # relu, small: fused
     assert _bwd_ws(capi, act="gelu") == 64 * 256 * 2                   # transcendental: materialised
     big = dict(M=4096, N=4096, K=4096)
     assert _bwd_ws(capi, **big) == 4096 * 4096 * 2                     # >= 2^30: materialised
-    assert _bwd_ws(capi, gBias=1 << 33, bias_kind=3, **big) == 4096 * 4096 * 2 + 64 * 4096 * 4
-    assert _bwd_ws(capi, gBias=1 << 33, bias_kind=3, gY=(1 << 28) + 2, **big) == 4096 * 4096 * 2  # unaligned: no partials
-    assert _bwd_ws(capi, act="tanh", M=3, N=10) == 256                 # rounded up to 256 bytes
+    pern = dict(gBias=1 << 33, bias_kind=3)
+    assert _bwd_ws(capi, **pern, **big) == 4096 * 4096 * 2             # partials in the dX output
+    assert _bwd_ws(capi, **pern, gA=0, **big) == 4096 * 4096 * 2       # ... or in the dW output
+    assert _bwd_ws(capi, **pern, ldga=4100, ldgb=4100, **big) == 4096 * 4096 * 2 + 64 * 4096 * 4  # padded
+    assert _bwd_ws(capi, **pern, gY=(1 << 28) + 2, **big) == 4096 * 4096 * 2  # unaligned: no partials
+    assert _bwd_ws(capi, act="tanh", M=3, N=10) == 3 * 10 * 2          # dY' only
     assert _bwd_ws(capi, act="gelu", gA=0, gB=0) == 0                  # nothing to multiply
     assert _bwd_ws(capi, dtype=7) == -1
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("act", ["gelu", "sigmoid", "relu"])
+@pytest.mark.parametrize("shape", [(64, 256, 784), (1024, 1024, 1024), (4096, 4096, 4096), (8, 512, 1024),
+                                   (33, 45, 70), (1, 64, 96)])
+def test_backward_into_dz_always_suffices(capi, dtype, act, shape):
+    """The reference's capture-safe backward passes an M*N fp32 dZ buffer as the scratch
+    (gemm_pybind.cpp:415-418, gemm/api.hpp:166-188): the operator's need never exceeds it when
+    dX and dW are dense, so backward_into never reaches the library's own buffer."""
+    M, N, K = shape
+    ws = _bwd_ws(capi, dtype=dtype, act=act, M=M, N=N, K=K, gBias=1 << 33, bias_kind=3)
+    assert 0 <= ws <= M * N * 4, (ws, M * N * 4)
+    ws = _bwd_ws(capi, dtype=dtype, act=act, M=M, N=N, K=K, gBias=1 << 33, bias_kind=3, gA=0)
+    assert 0 <= ws <= M * N * 4, (ws, M * N * 4)
 
 
 def test_missing_library_fails_loudly(capi, monkeypatch, tmp_path):

@@ -188,6 +188,29 @@ def test_backward(gpu, case):
         assert np.array_equal(gC[pos], gY[pos]) and np.all(gC[~pos] == 0)
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=lambda d: DT_NAMES[d])
+def test_backward_gc_beta_zero(gpu, dtype):
+    """beta = 0 (no C in the forward): gC is zero-filled, as the reference's backward does
+    (regemm_backward.cu:183-189), even where dY is inf or NaN."""
+    capi = gpu
+    M, N, K = 24, 40, 16
+    g = np.random.default_rng(17)
+    gY = rounded(g.standard_normal((M, N)), dtype)
+    gY[0, :4] = [np.inf, -np.inf, np.nan, 1.0]
+    Z = rounded(g.standard_normal((M, N)), dtype)
+    es = capi.elem_bytes(dtype)
+    dev = Dev(capi)
+    try:
+        pgY, pZ = dev.put(capi.to_storage(gY, dtype)), dev.put(capi.to_storage(Z, dtype))
+        pgC = dev.empty(M * N * es)
+        capi.gemm_bwd(dtype=dtype, M=M, N=N, K=K, A=0, B=0, gY=pgY, Z=pZ, gC=pgC, act="relu", beta=0.0)
+        capi.synchronize()
+        gC = dev.get(pgC, (M, N), dtype)
+    finally:
+        dev.close()
+    assert np.all(gC == 0) and not np.any(np.signbit(gC))
+
+
 # ---------------------------------------------------------------------------
 # Batched / strided forms (exact-integer inputs: results must be bit-exact)
 # ---------------------------------------------------------------------------
