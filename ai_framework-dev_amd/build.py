@@ -31,9 +31,8 @@ INCLUDE = os.path.join(REPO, "include")
 HIP_SOURCES = [
     "gemm_tile_f32.hip", "gemm_tile_bf16.hip", "gemm_tile_f16.hip",
     "gemm_dl_bf16.hip", "gemm_dl_f16.hip",
-    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "conv.hip", "rnn.hip", "attn.hip", "probe.hip",
+    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "noalloc.hip", "conv.hip", "rnn.hip", "attn.hip", "probe.hip",
 ]
-HIP_HEADERS = ["gev2_device.hpp", "gev2_kernels.hpp", "gemm_tile_impl.hpp", "gemm_dl_impl.hpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function",
@@ -51,6 +50,19 @@ BIND_SOURCES = {
 }
 HOST_HEADERS = ["host/shim.hpp", "host/gemm_host.hpp", "host/conv2d_host.hpp", "host/rnn_host.hpp",
                 "host/sdpa_host.hpp"]
+
+
+def _includes(path: str, seen=None) -> list[str]:
+    """The file and every local header it includes (#include "..."), recursively."""
+    import re
+    seen = set() if seen is None else seen
+    if path in seen or not os.path.exists(path):
+        return []
+    seen.add(path)
+    with open(path) as f:
+        for inc in re.findall(r'^\s*#\s*include\s+"([^"]+)"', f.read(), re.M):
+            _includes(os.path.normpath(os.path.join(os.path.dirname(path), inc)), seen)
+    return sorted(seen)
 
 
 def _newer(target: str, deps: list[str]) -> bool:
@@ -72,13 +84,12 @@ def _run(cmd: list[str]) -> None:
 def build_hip(force: bool, jobs: int) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     os.makedirs(OUT_DIR, exist_ok=True)
-    headers = [os.path.join(CSRC, h) for h in HIP_HEADERS] + [os.path.join(INCLUDE, "gev2_gemm.h")]
     objs, todo = [], []
     for src in HIP_SOURCES:
         s = os.path.join(CSRC, src)
         o = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
         objs.append(o)
-        if force or _newer(o, [s] + headers):
+        if force or _newer(o, _includes(s)):
             todo.append([HIPCC, *HIP_FLAGS, "-c", s, "-o", o])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, todo))

@@ -302,7 +302,19 @@ const char* gev2_status_string(int s) {
   }
 }
 
-int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
+int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) { return gev2::gemm_fwd_run(d, stream, nullptr, -1); }
+
+}  // extern "C"
+
+namespace gev2 {
+
+int report_hip_error(hipError_t e, const char* where) { return hip_fail(e, where); }
+
+// The forward.  fixed_bytes < 0: scratch from the caller's workspace, else the
+// per-stream buffer (or the scratch-free kernel under capture).  fixed_bytes
+// >= 0: scratch only from `fixed` (fixed_bytes of it), nothing allocated, and
+// a problem that needs more is refused.
+int gemm_fwd_run(const gev2_gemm_fwd_desc* d, void* stream, void* fixed, int64_t fixed_bytes) {
   t_last_error.clear();
   FwdPlan pl;
   int st = plan_fwd(d, &pl);
@@ -317,7 +329,13 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   // ---- skinny path ----
   if (pl.skinny) {
     float* part = nullptr;
-    if (pl.ws_bytes > 0) {
+    if (pl.ws_bytes > 0 && fixed_bytes >= 0) {
+      if (pl.ws_bytes > fixed_bytes)
+        return fail(GEV2_INVALID_ARGUMENT, "the problem needs " + std::to_string(pl.ws_bytes) +
+                                               " bytes of split-K scratch, more than the " +
+                                               std::to_string(fixed_bytes) + " bytes available");
+      part = static_cast<float*>(fixed);
+    } else if (pl.ws_bytes > 0) {
       if (aligned256(d->workspace) && d->workspace_bytes >= pl.ws_bytes) {
         part = static_cast<float*>(d->workspace);
       } else if (stream_capturing(s)) {
@@ -364,7 +382,7 @@ int gev2_gemm_fwd(const gev2_gemm_fwd_desc* d, void* stream) {
   return GEV2_OK;
 }
 
-}  // extern "C"
+}  // namespace gev2
 
 namespace {
 

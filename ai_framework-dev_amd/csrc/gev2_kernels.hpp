@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+struct gev2_gemm_fwd_desc;   // include/gev2_gemm.h
+
 namespace gev2 {
 
 // One launch of the MFMA tile kernel computes, for each batch slice b,
@@ -106,6 +108,18 @@ hipError_t launch_dl_f16(int cfg, bool ta, bool tb, const TileArgs& a, int batch
 bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a);
 // part: fp32 partial sums for the split-K 16-bit kernel (skinny_split_workspace_bytes)
 hipError_t launch_skinny(int dtype, const SkinnyArgs& a, float* part, hipStream_t s);
+
+// Size of the fixed device array that gev2_gemm_fwd_noalloc takes its split-K
+// scratch from (noalloc.hip): 16 MiB, the partials of skinny problems up to
+// N * K = 2^26 at M = 16 (2 MiB at M = 8, N = K = 4096).
+constexpr int64_t kNoAllocScratchBytes = int64_t{16} << 20;
+
+// The forward of gev2_gemm_fwd (capi.hip).  fixed_bytes < 0: split-K scratch
+// from the caller's workspace or the library's per-stream buffer; fixed_bytes
+// >= 0: only from `fixed` (no allocation; larger needs are refused).
+int gemm_fwd_run(const ::gev2_gemm_fwd_desc* d, void* stream, void* fixed, int64_t fixed_bytes);
+// Records a HIP error as the calling thread's last error; returns GEV2_HIP_ERROR.
+int report_hip_error(hipError_t e, const char* where);
 bool skinny_split_eligible(const SkinnyArgs& a);
 int64_t skinny_split_workspace_bytes(int M, int N, int K);
 hipError_t launch_grad_elementwise(int dtype, const GradArgs& a, int batch, hipStream_t s);

@@ -20,7 +20,7 @@ ACT = {"none": 0, "relu": 1, "leakyrelu": 2, "leaky_relu": 2, "lrelu": 2, "gelu"
 BIAS_NONE, BIAS_SCALAR, BIAS_PERM, BIAS_PERN = 0, 1, 2, 3
 
 EXPORTED = [
-    "gev2_gemm_fwd", "gev2_gemm_bwd", "gev2_gemm_fwd_workspace_size", "gev2_gemm_fwd_repeat", "gev2_gemm_bwd_repeat", "gev2_abi_version", "gev2_status_string",
+    "gev2_gemm_fwd", "gev2_gemm_fwd_noalloc", "gev2_gemm_bwd", "gev2_gemm_fwd_workspace_size", "gev2_gemm_fwd_repeat", "gev2_gemm_bwd_repeat", "gev2_abi_version", "gev2_status_string",
     "gev2_last_error", "gev2_last_path", "gev2_device_count", "gev2_set_device",
     "gev2_get_device", "gev2_device_info", "gev2_malloc", "gev2_free", "gev2_memcpy_htod",
     "gev2_memcpy_dtoh", "gev2_memcpy_dtod_async", "gev2_memset", "gev2_stream_create",
@@ -163,6 +163,7 @@ def lib() -> ctypes.CDLL:
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     L.gev2_gemm_fwd.argtypes = [ctypes.POINTER(FwdDesc), vp]
+    L.gev2_gemm_fwd_noalloc.argtypes = [ctypes.POINTER(FwdDesc), vp]
     L.gev2_gemm_bwd.argtypes = [ctypes.POINTER(BwdDesc), vp]
     L.gev2_gemm_fwd_workspace_size.argtypes = [ctypes.POINTER(FwdDesc)]
     L.gev2_gemm_fwd_workspace_size.restype = i64
@@ -414,6 +415,13 @@ def bwd_desc(*, dtype: int, M: int, N: int, K: int, A: int, B: int, gY: int, Z: 
 def gemm_fwd(*, stream: int = 0, **kw) -> None:
     d = fwd_desc(**kw)
     check(lib().gev2_gemm_fwd(ctypes.byref(d), stream or None), "gev2_gemm_fwd")
+
+
+def gemm_fwd_noalloc(*, stream: int = 0, **kw) -> None:
+    """gev2_gemm_fwd_noalloc: the forward with its split-K scratch in the library's fixed
+    device array (no allocation; desc.workspace ignored)."""
+    d = fwd_desc(**kw)
+    check(lib().gev2_gemm_fwd_noalloc(ctypes.byref(d), stream or None), "gev2_gemm_fwd_noalloc")
 
 
 def gemm_bwd(*, stream: int = 0, **kw) -> None:

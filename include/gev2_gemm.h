@@ -153,6 +153,18 @@ typedef struct gev2_gemm_bwd_desc {
 } gev2_gemm_bwd_desc;
 
 int gev2_gemm_fwd(const gev2_gemm_fwd_desc* desc, void* stream);
+/* The forward above, allocating nothing, ever.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The only
+ * scratch the forward uses, the split-K partial sums of skinny 16-bit
+ * problems (gev2_gemm_fwd_workspace_size), is taken from a fixed 16 MiB device
+ * array that each GPU holds until the process ends; desc->workspace is
+ * ignored.  A problem needing more than 16 MiB of it returns
+ * GEV2_INVALID_ARGUMENT (2 MiB at M = 8, N = K = 4096).  Every call on a GPU
+ * shares that GPU's array and overwrites what it uses (nothing needs to start
+ * at zero), so calls that overlap on one GPU (on different streams) race.
+ * Results are bit-identical to gev2_gemm_fwd's. */
+int gev2_gemm_fwd_noalloc(const gev2_gemm_fwd_desc* desc, void* stream);
 /* Scratch bytes gev2_gemm_fwd uses for `desc` (0: none); -1 for an invalid
  * descriptor.  No counterpart in the reference (its forward needs none). */
 int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* desc);
