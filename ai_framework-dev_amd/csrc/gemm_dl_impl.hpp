@@ -190,8 +190,8 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FM][FN], co
 //   q = NQ-1: MFMAs of the last step | step-0 reads of tile t+1 | loads of
 //   tile t+S into stage t % S
 // so a tile's loads are issued S-1 tiles before it is read.
-template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S>
-__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S, int WPE>
+__global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_dl_kernel(TileArgs p) {
   static_assert(sizeof(T) == 2, "16-bit element types only");
   constexpr int NT = WM * WN * 64;
@@ -319,26 +319,29 @@ gemm_dl_kernel(TileArgs p) {
   }
 }
 
-// K depth and stage count per tile shape: the most stages of BK = 32 that fit
-// in LDS (two 128x128 workgroups share a CU).
-// GEV2_DL256_BK / GEV2_DL256_S override the 256x256 choice at build time
-// (tuning builds).
-#ifndef GEV2_DL256_BK
-#define GEV2_DL256_BK 64
-#define GEV2_DL256_S 2
-#endif
+// Waves, K depth and stage count per tile shape.
+//   256x256: 8 waves of 128x64 (2 per SIMD, accumulators in VGPRs), two stages
+//     of BK = 64 (128 KB).  A second wave per SIMD keeps the MFMA pipe fed
+//     while the other waits on its fragment reads or the tile barrier, and
+//     halves each wave's share of the epilogue: measured at 4096^3 bf16
+//     (interleaved runs, medians) 123.9 us against 129.1 us for 4 waves of
+//     128x128 (one per SIMD); per-wave timestamps put the 4-wave epilogue at
+//     27.8k cycles and the 8-wave one at 18.0k.  BK = 32 with 4 stages gave
+//     127.7 us, 16 waves with 5 stages 143 us.
+//   128x256 / 128x128: 4 waves, the most stages of BK = 32 that fit in LDS
+//     (two 128x128 workgroups share a CU).
 template <int CFG> struct DlPipe;
-template <> struct DlPipe<kCfg256x256> { static constexpr int BK = GEV2_DL256_BK, S = GEV2_DL256_S; };
-template <> struct DlPipe<kCfg128x256> { static constexpr int BK = 32, S = 6; };
-template <> struct DlPipe<kCfg128x128> { static constexpr int BK = 32, S = 4; };
+template <> struct DlPipe<kCfg256x256> { static constexpr int BK = 64, S = 2, WM = 2, WN = 4, WPE = 2; };
+template <> struct DlPipe<kCfg128x256> { static constexpr int BK = 32, S = 6, WM = 2, WN = 2, WPE = 1; };
+template <> struct DlPipe<kCfg128x128> { static constexpr int BK = 32, S = 4, WM = 2, WN = 2, WPE = 1; };
 
 template <typename T, int CFG, bool TA, bool TB>
 static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
   using C = CfgShape<CFG>;
   using P = DlPipe<CFG>;
   dim3 grid(a.tiles_m * a.tiles_n, batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, C::WM, C::WN, TA, TB, P::BK, P::S>), grid,
-                     dim3(C::WM * C::WN * 64), 0, s, a);
+  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, P::WM, P::WN, TA, TB, P::BK, P::S, P::WPE>), grid,
+                     dim3(P::WM * P::WN * 64), 0, s, a);
   return hipGetLastError();
 }
 
