@@ -179,29 +179,45 @@ bool aligned256(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 2
 // the caller passes no workspace: one buffer per (device, stream), grown on
 // demand (a stream runs its calls in order, so they can share it).  hipFree
 // waits for queued work that may still read the old buffer.
-// It is never used while the stream is being captured: the operator then
-// takes a path that needs no scratch (or the caller's workspace), so no graph
-// ever refers to one of these buffers and growing one cannot leave a graph
-// pointing at freed memory.
-std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_stream_ws;
+// While the stream is being captured nothing is allocated: a buffer that an
+// earlier eager call left large enough is used (so the graph records the same
+// kernels as the eager call), and from then on it is pinned: a later growth
+// or gev2_stream_destroy retires it without freeing it, since a graph may
+// still use it.  Without such a buffer the caller takes a scratch-free path.
+struct StreamWs {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  bool pinned = false;
+};
+std::map<std::pair<int, hipStream_t>, StreamWs> g_stream_ws;
+std::vector<void*> g_pinned_retired;   // kept until the process ends
 
-int get_stream_ws(hipStream_t s, size_t bytes, void** out) {
-  if (stream_capturing(s))
-    return fail(GEV2_MISSING_INPUT, "the stream is being captured into a graph and no workspace of " +
-                                        std::to_string(bytes) + " bytes was passed (nothing is allocated during capture)");
+// *out = the stream's buffer of at least `bytes`, or nullptr when the stream
+// is being captured and no such buffer exists yet.
+int acquire_stream_ws(hipStream_t s, size_t bytes, void** out) {
+  *out = nullptr;
+  const bool capturing = stream_capturing(s);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto& ws = g_stream_ws[{dev, s}];
-  if (ws.second < bytes) {
-    if (ws.first) (void)hipFree(ws.first);
-    ws = {nullptr, 0};
-    e = hipMalloc(&ws.first, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-    ws.second = bytes;
+  StreamWs& ws = g_stream_ws[{dev, s}];
+  if (ws.bytes < bytes) {
+    if (capturing) return GEV2_OK;
+    if (ws.ptr) {
+      if (ws.pinned) g_pinned_retired.push_back(ws.ptr);
+      else (void)hipFree(ws.ptr);
+    }
+    ws = StreamWs{};
+    e = hipMalloc(&ws.ptr, bytes);
+    if (e != hipSuccess) {
+      ws = StreamWs{};
+      return hip_fail(e, "hipMalloc(workspace)");
+    }
+    ws.bytes = bytes;
   }
-  *out = ws.first;
+  if (capturing) ws.pinned = true;
+  *out = ws.ptr;
   return GEV2_OK;
 }
 
@@ -227,7 +243,53 @@ struct FwdPlan {
   int64_t lda = 0, ldb = 0, ldy = 0, ldz = 0;
   int64_t ws_bytes = 0;
   gev2::SkinnyArgs sk{};
+  // fp32 split-K on the tile path: ksplit slices of kc (the last kc_last),
+  // partial products [ksplit][M][N] fp32 in the workspace (ws_bytes)
+  int ksplit = 0;
+  int64_t kc = 0, kc_last = 0;
 };
+
+// Slices of a split reduction of depth R over `tiles` output tiles: enough
+// slices for about 128 workgroups, each at least 16 deep.  A slice depth (a
+// multiple of 4) that divides R, with a count within [want/2, 2 want] nearest
+// want, keeps every slice in one batched launch; otherwise slices of a
+// multiple of 16 and a separate launch for the shorter tail.  False: no split.
+bool splitk_slices(int64_t R, int64_t tiles, int64_t* kc_out, int64_t* ks_out) {
+  const int64_t want = std::max<int64_t>(2, std::min<int64_t>(R / 32, 128 / std::max<int64_t>(tiles, 1)));
+  int64_t kc = 0;
+  for (int64_t c = 16; c <= R / 2; c += 4) {
+    const int64_t n = R / c;
+    if (R % c || 2 * n < want || n > 2 * want) continue;
+    if (!kc || std::llabs(n - want) < std::llabs(R / kc - want)) kc = c;
+  }
+  if (!kc) kc = ((R + want - 1) / want + 15) / 16 * 16;
+  const int64_t ks = (R + kc - 1) / kc;
+  if (ks < 2) return false;
+  *kc_out = kc;
+  *ks_out = ks;
+  return true;
+}
+
+// fp32 problems too small to occupy the GPU with 64x64 tiles (C1: 4 tiles on
+// 256 CUs, each running K = 784 alone) split K over workgroups: slices of kc
+// run as one batched launch into fp32 partials, and a
+// second pass adds the slices in order and applies alpha, bias, Z and act.
+void plan_splitk(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
+  const int64_t M = d->M, N = d->N, K = d->K;
+  if (d->dtype != GEV2_F32 || d->batch != 1 || d->trans_a || d->trans_b || env_int("GEV2_NO_SPLITK", 0) != 0)
+    return;
+  const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles > 32 || K < 256) return;
+  if (!vec_ok(d->A, pl->lda, 0, K, M, 1, d->dtype) || !vec_ok(d->B, pl->ldb, 0, N, K, 1, d->dtype)) return;
+  if (out_level(d->Y, pl->ldy, 0, M, N, 1, d->dtype) == 0 || out_level(d->Z, pl->ldz, 0, M, N, 1, d->dtype) == 0)
+    return;
+  int64_t kc = 0, ks = 0;
+  if (!splitk_slices(K, tiles, &kc, &ks)) return;
+  pl->ksplit = static_cast<int>(ks);
+  pl->kc = kc;
+  pl->kc_last = K - (ks - 1) * kc;
+  pl->ws_bytes = ks * M * N * 4;
+}
 
 int plan_fwd(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
   if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
@@ -250,7 +312,10 @@ int plan_fwd(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
   const int epc = elems_per_chunk(d->dtype);
   pl->skinny = d->batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 && N % epc == 0 &&
                vec_ok(d->B, pl->ldb, 0, N, K, 1, d->dtype) && env_int("GEV2_NO_SKINNY", 0) == 0;
-  if (!pl->skinny) return GEV2_OK;
+  if (!pl->skinny) {
+    plan_splitk(d, pl);
+    return GEV2_OK;
+  }
   const bool has_bias = d->bias && d->bias_kind != GEV2_BIAS_NONE;
   gev2::SkinnyArgs& a = pl->sk;
   a.A = d->A; a.B = d->B; a.D = d->Y; a.Zo = d->Z;
@@ -278,7 +343,7 @@ int64_t gev2_gemm_fwd_workspace_size(const gev2_gemm_fwd_desc* d) {
   t_last_error.clear();
   FwdPlan pl;
   if (plan_fwd(d, &pl) != GEV2_OK) return -1;
-  return (pl.empty || !pl.skinny) ? 0 : pl.ws_bytes;
+  return pl.empty ? 0 : pl.ws_bytes;
 }
 const char* gev2_last_path(void) { return t_last_path; }
 
@@ -338,21 +403,74 @@ int gemm_fwd_run(const gev2_gemm_fwd_desc* d, void* stream, void* fixed, int64_t
     } else if (pl.ws_bytes > 0) {
       if (aligned256(d->workspace) && d->workspace_bytes >= pl.ws_bytes) {
         part = static_cast<float*>(d->workspace);
-      } else if (stream_capturing(s)) {
-        // no workspace under capture: the dot-product kernel, which needs none
-        pl.sk.x_vec = std::min(pl.sk.x_vec, 1);
-        pl.split = false;
       } else {
         void* w = nullptr;
-        st = get_stream_ws(s, static_cast<size_t>(pl.ws_bytes), &w);
+        st = acquire_stream_ws(s, static_cast<size_t>(pl.ws_bytes), &w);
         if (st != GEV2_OK) return st;
         part = static_cast<float*>(w);
+        if (!part) {
+          // no scratch under capture: the dot-product kernel, which needs none
+          pl.sk.x_vec = std::min(pl.sk.x_vec, 1);
+          pl.split = false;
+        }
       }
     }
     hipError_t e = gev2::launch_skinny(d->dtype, pl.sk, part, s);
     if (e != hipSuccess) return hip_fail(e, "skinny launch");
     t_last_path = pl.split ? "skinny:split" : "skinny";
     return GEV2_OK;
+  }
+
+  // ---- fp32 split-K (small problems): partials in the workspace, else the
+  // per-stream buffer; under capture (or past the no-allocation array) the
+  // plain tile path below ----
+  if (pl.ksplit > 0) {
+    float* part = nullptr;
+    if (fixed_bytes >= 0) {
+      if (pl.ws_bytes <= fixed_bytes) part = static_cast<float*>(fixed);
+    } else if (aligned256(d->workspace) && d->workspace_bytes >= pl.ws_bytes) {
+      part = static_cast<float*>(d->workspace);
+    } else {
+      void* w = nullptr;
+      st = acquire_stream_ws(s, static_cast<size_t>(pl.ws_bytes), &w);
+      if (st != GEV2_OK) return st;
+      part = static_cast<float*>(w);
+    }
+    if (part) {
+      const int ks = pl.ksplit;
+      const int full = pl.kc_last == pl.kc ? ks : ks - 1;   // slices of depth kc
+      const int cfg = pick_cfg(GEV2_F32, M, N, full);
+      gev2::TileArgs a{};
+      a.A = d->A; a.B = d->B; a.D = part;
+      a.lda = lda; a.ldb = ldb; a.ldd = N;
+      a.sA = pl.kc; a.sB = pl.kc * ldb; a.sD = M * N;
+      a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(pl.kc);
+      a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = 1.f; a.slope = 0.f; a.pro_act = 0;
+      const int bm = gev2::tile_bm(cfg, true), bn = gev2::tile_bn(cfg, true);
+      a.tiles_m = static_cast<int>((M + bm - 1) / bm);
+      a.tiles_n = static_cast<int>((N + bn - 1) / bn);
+      a.store_vec = 1;
+      hipError_t e = gev2::launch_tile(GEV2_F32, cfg, false, false, 0, true, a, full, s);
+      if (e != hipSuccess) return hip_fail(e, "split-K launch");
+      if (full < ks) {
+        gev2::TileArgs r = a;
+        r.A = static_cast<const float*>(d->A) + (int64_t)full * pl.kc;
+        r.B = static_cast<const float*>(d->B) + (int64_t)full * pl.kc * ldb;
+        r.D = part + (int64_t)full * M * N;
+        r.K = static_cast<int>(pl.kc_last);
+        e = gev2::launch_tile(GEV2_F32, cfg, false, false, 0, true, r, 1, s);
+        if (e != hipSuccess) return hip_fail(e, "split-K launch");
+      }
+      gev2::SplitkReduceArgs ra{};
+      ra.part = part; ra.ks = ks; ra.M = static_cast<int>(M); ra.N = static_cast<int>(N);
+      ra.alpha = d->alpha; ra.bias = has_bias ? d->bias : nullptr; ra.bias_kind = has_bias ? d->bias_kind : 0;
+      ra.act = d->act; ra.slope = d->leaky_slope;
+      ra.Y = static_cast<float*>(d->Y); ra.ldy = ldy; ra.Z = static_cast<float*>(d->Z); ra.ldz = ldz;
+      e = gev2::launch_splitk_reduce(ra, s);
+      if (e != hipSuccess) return hip_fail(e, "split-K reduction launch");
+      t_last_path = "tile:splitk";
+      return GEV2_OK;
+    }
   }
 
   // ---- tile path ----
@@ -405,6 +523,10 @@ struct BwdScratch {
   int64_t gz_bytes{0};     // dY': batch*M*N elements
   int64_t part_bytes{0};   // dBias partials (sums only)
   int64_t need{0};         // what gev2_gemm_bwd_workspace_size reports
+  // fp32 dX split over the reduction (N) when dY' is formed while loading:
+  // dx_ks slices of dx_kc (the last dx_kc_last), partials [dx_ks][M][K] fp32
+  int dx_ks{0};
+  int64_t dx_kc{0}, dx_kc_last{0}, dx_bytes{0};
 };
 
 int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -420,7 +542,26 @@ BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
   const bool linear = d->act == GEV2_ACT_NONE || d->act == GEV2_ACT_RELU || d->act == GEV2_ACT_LEAKY_RELU;
   const double work = static_cast<double>(M) * N * K * batch;
   r.materialise = (!linear || work >= (1u << 30)) && (d->gA || d->gB) && env_int("GEV2_FUSED_BWD", 0) == 0;
-  if (!r.materialise) return r;
+  if (!r.materialise) {
+    // small fp32 problems: dX (few 64x64 tiles, long reduction over N) split
+    // over workgroups, with the partials in the otherwise unused workspace
+    const int64_t lda_b = dense_ld(d->ldb, N), ldga = dense_ld(d->ldga, K);
+    const int64_t tiles = ((M + 63) / 64) * ((K + 63) / 64);
+    if (dt == GEV2_F32 && batch == 1 && d->gA && M > gev2::kSkinnyMaxM && tiles <= 32 && N >= 256 &&
+        !scalar_loads && env_int("GEV2_NO_SPLITK", 0) == 0 && vec_ok(d->gY, ldgy, 0, N, M, 1, dt) &&
+        vec_ok(d->Z, ldz, 0, N, M, 1, dt) && vec_ok(d->B, lda_b, 0, N, K, 1, dt) &&
+        out_level(d->gA, ldga, 0, M, K, 1, dt) > 0) {
+      int64_t kc = 0, ks = 0;
+      if (splitk_slices(N, tiles, &kc, &ks)) {
+        r.dx_ks = static_cast<int>(ks);
+        r.dx_kc = kc;
+        r.dx_kc_last = N - (ks - 1) * kc;
+        r.dx_bytes = ks * M * K * 4;
+        r.need = r.dx_bytes;
+      }
+    }
+    return r;
+  }
   const int epc = elems_per_chunk(dt);
   r.prep_vec = !scalar_loads && N % epc == 0 && vec_ok(d->gY, ldgy, d->stride_gy, N, M, batch, dt) &&
                vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt);
@@ -494,9 +635,9 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   bool bias_done = false;
   const BwdScratch sc = bwd_scratch(d);
   // Where dY' goes: the caller's workspace when it holds dY'; otherwise the
-  // per-stream buffer, except under graph capture, where the GEMMs apply act'
-  // to dY on load instead for none / ReLU / LeakyReLU, and the transcendental
-  // activations are refused (nothing is allocated during capture).
+  // per-stream buffer.  Under graph capture without either (nothing is
+  // allocated then) the GEMMs apply act' to dY on load instead for none /
+  // ReLU / LeakyReLU, and the transcendental activations are refused.
   void* ws = nullptr;
   bool sums = sc.sums;
   if (sc.materialise) {
@@ -505,11 +646,13 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       // partials parked after dY' need the larger size; without it dBias
       // falls back to the column-sum kernel below
       if (sums && sc.part_home == kPartWorkspace && d->workspace_bytes < sc.need) sums = false;
-    } else if (!stream_capturing(s)) {
-      st = get_stream_ws(s, static_cast<size_t>(sc.need), &ws);
+    } else {
+      st = acquire_stream_ws(s, static_cast<size_t>(sc.need), &ws);
       if (st != GEV2_OK) return st;
-    } else if (!linear) {
-      // act' is applied on load for the piecewise-linear activations only
+    }
+    if (!ws && !linear) {
+      // under capture with no scratch: act' is applied on load for the
+      // piecewise-linear activations only
       return fail(GEV2_MISSING_INPUT, "the stream is being captured into a graph: a GELU / Sigmoid / Tanh backward "
                                       "needs a dY' workspace of " + std::to_string(sc.gz_bytes) +
                                       " bytes (nothing is allocated during capture)");
@@ -558,6 +701,22 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   const bool gyz_vec = vec_ok(G, ldG, sG, N, M, batch, dt) &&
                        (!fused || vec_ok(d->Z, ldz, d->stride_z, N, M, batch, dt)) && !scalar_loads;
 
+  // scratch of the fp32 dX split: the caller's workspace, else the stream's
+  // buffer (none under capture without one: the unsplit launch then)
+  // (a caller workspace too small for them means no split: a call that passes
+  // scratch, like the reference's capture-safe backward with its M*N dZ,
+  // never reaches the library's buffer)
+  float* dx_part = nullptr;
+  if (d->gA && fused && sc.dx_ks > 0) {
+    if (aligned256(d->workspace) && d->workspace_bytes >= sc.dx_bytes) {
+      dx_part = static_cast<float*>(d->workspace);
+    } else if (!d->workspace) {
+      void* w = nullptr;
+      st = acquire_stream_ws(s, static_cast<size_t>(sc.dx_bytes), &w);
+      if (st != GEV2_OK) return st;
+      dx_part = static_cast<float*>(w);
+    }
+  }
   // gA[M,K] = alpha * dY' [M,N] * B^T : NT (prologue on A when fused)
   if (d->gA) {
     const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, K, batch, dt);
@@ -570,6 +729,41 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       n.act = d->act; n.slope = d->leaky_slope; n.alpha = d->alpha;
       hipError_t e = gev2::launch_skinny_nt(dt, n, s);
       if (e != hipSuccess) return hip_fail(e, "dX skinny launch");
+    } else if (float* part = dx_part) {
+      // dX split over N: slices into fp32 partials, then an ordered sum (alpha)
+      const int ks = sc.dx_ks;
+      const int full = sc.dx_kc_last == sc.dx_kc ? ks : ks - 1;
+      const int cfg = pick_cfg(dt, M, K, full, true);
+      gev2::TileArgs a{};
+      a.A = G; a.lda = ldG; a.sA = sc.dx_kc;
+      a.Zi = d->Z; a.ldzi = ldz; a.sZi = sc.dx_kc;
+      a.B = d->B; a.ldb = ldb; a.sB = sc.dx_kc;
+      a.D = part; a.ldd = K; a.sD = M * K;
+      a.M = static_cast<int>(M); a.N = static_cast<int>(K); a.K = static_cast<int>(sc.dx_kc);
+      a.act = GEV2_ACT_NONE; a.bias_kind = GEV2_BIAS_NONE; a.alpha = 1.f;
+      a.slope = d->leaky_slope; a.pro_act = d->act;
+      const int bm = gev2::tile_bm(cfg, true), bn = gev2::tile_bn(cfg, true);
+      a.tiles_m = static_cast<int>((M + bm - 1) / bm);
+      a.tiles_n = static_cast<int>((K + bn - 1) / bn);
+      a.store_vec = 1;
+      hipError_t e = gev2::launch_tile(dt, cfg, false, true, 1, true, a, full, s);
+      if (e != hipSuccess) return hip_fail(e, "dX split launch");
+      if (full < ks) {
+        gev2::TileArgs r = a;
+        r.A = static_cast<const float*>(G) + (int64_t)full * sc.dx_kc;
+        r.Zi = static_cast<const float*>(d->Z) + (int64_t)full * sc.dx_kc;
+        r.B = static_cast<const float*>(d->B) + (int64_t)full * sc.dx_kc;
+        r.D = part + (int64_t)full * M * K;
+        r.K = static_cast<int>(sc.dx_kc_last);
+        e = gev2::launch_tile(dt, cfg, false, true, 1, true, r, 1, s);
+        if (e != hipSuccess) return hip_fail(e, "dX split launch");
+      }
+      gev2::SplitkReduceArgs ra{};
+      ra.part = part; ra.ks = ks; ra.M = static_cast<int>(M); ra.N = static_cast<int>(K);
+      ra.alpha = d->alpha; ra.bias = nullptr; ra.bias_kind = 0; ra.act = GEV2_ACT_NONE; ra.slope = 0.f;
+      ra.Y = static_cast<float*>(d->gA); ra.ldy = ldga; ra.Z = nullptr; ra.ldz = 0;
+      e = gev2::launch_splitk_reduce(ra, s);
+      if (e != hipSuccess) return hip_fail(e, "dX split reduction launch");
     } else {
       const int cfg = pick_cfg(dt, M, K, batch, fused);
       gev2::TileArgs a{};
@@ -720,7 +914,8 @@ int gev2_stream_destroy(void* stream) {
     for (auto it = g_stream_ws.begin(); it != g_stream_ws.end();) {
       if (it->first.second == reinterpret_cast<hipStream_t>(stream)) {
         (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
-        if (it->second.first) (void)hipFree(it->second.first);
+        if (it->second.pinned) g_pinned_retired.push_back(it->second.ptr);
+        else if (it->second.ptr) (void)hipFree(it->second.ptr);
         it = g_stream_ws.erase(it);
       } else {
         ++it;
@@ -765,8 +960,8 @@ int gev2_event_elapsed_ms(float* ms, void* start, void* stop) {
 
 // HIP graph capture of a stream's work (thread-local capture mode: other
 // threads' HIP calls are unaffected).  The operator calls allocate nothing
-// while their stream is capturing (get_stream_ws refuses; the forward and
-// backward take their scratch-free paths instead).
+// while their stream is capturing (acquire_stream_ws; without scratch the
+// forward and backward take their scratch-free paths).
 int gev2_graph_begin(void* stream) {
   if (!stream) return fail(GEV2_INVALID_ARGUMENT, "capture needs a created stream, not the null stream");
   GEV2_HIP_CALL(hipStreamBeginCapture(reinterpret_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),

@@ -241,6 +241,37 @@ hipError_t launch_skinny_nt(int dtype, const SkinnyNtArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// fp32 split-K reduction: one thread per output element (64 threads per
+// workgroup, so even a 64x256 output spreads over 256 workgroups); the ks
+// slices are added in order s = 0, 1, ... with 16 loads in flight, then alpha,
+// bias, Z and act.
+__global__ void __launch_bounds__(64) splitk_reduce_kernel(SplitkReduceArgs p) {
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i >= (int64_t)p.M * p.N) return;
+  const int m = static_cast<int>(i / p.N), n = static_cast<int>(i - (int64_t)m * p.N);
+  const int64_t slice = (int64_t)p.M * p.N;
+  const float* src = p.part + i;
+  float acc = src[0];
+  for (int s0 = 1; s0 < p.ks; s0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = s0 + u < p.ks ? src[(s0 + u) * slice] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (s0 + u < p.ks) acc += v[u];
+  }
+  const float b = p.bias ? load_bias(p.bias, p.bias_kind, m, n) : 0.f;
+  const float z = fmaf(p.alpha, acc, b);
+  if (p.Z) p.Z[(int64_t)m * p.ldz + n] = z;
+  p.Y[(int64_t)m * p.ldy + n] = act_fwd(z, p.act, p.slope);
+}
+
+hipError_t launch_splitk_reduce(const SplitkReduceArgs& a, hipStream_t s) {
+  const int64_t threads = (int64_t)a.M * a.N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>((threads + 63) / 64)), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
 template <typename T>
 static hipError_t grad_prep_t(const PrepArgs& a, int batch, hipStream_t s) {
   constexpr int COLS = 32 * Elem<T>::kPerChunk;

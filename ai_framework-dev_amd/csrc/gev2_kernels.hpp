@@ -83,6 +83,19 @@ struct SkinnyNtArgs {
   int act; float slope, alpha;
 };
 hipError_t launch_skinny_nt(int dtype, const SkinnyNtArgs& a, hipStream_t s);
+// Second pass of the fp32 split-K forward: Z = alpha * sum_s part[s] + bias
+// (slices added in order s = 0, 1, ...), Y = act(Z).  part is [ks][M][N]
+// dense; Y / Z are row-major with leading dimensions ldy / ldz (Z may be null).
+struct SplitkReduceArgs {
+  const float* part;
+  int ks, M, N;
+  float alpha;
+  const float* bias; int bias_kind;
+  int act; float slope;
+  float* Y; int64_t ldy;
+  float* Z; int64_t ldz;
+};
+hipError_t launch_splitk_reduce(const SplitkReduceArgs& a, hipStream_t s);
 hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
                                   float* gbias, int64_t sGbias, int batch, hipStream_t s);
 

@@ -25,16 +25,18 @@
  *     never throw; gev2_last_error() gives a message for the calling thread.
  *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = null stream).
  *   - Device memory is allocated only for scratch that the caller did not
- *     pass in `workspace`: the forward's split-K partial sums for skinny
- *     16-bit problems (gev2_gemm_fwd_workspace_size gives the size, 0 for all
- *     other problems) and the backward's materialised dY'.  Such a buffer is
- *     allocated once per (device, stream) and kept until gev2_stream_destroy.
- *   - Nothing is allocated while `stream` is being captured into a HIP graph,
- *     so a captured graph never refers to library-owned memory.  Without a
- *     large enough workspace the forward then uses its scratch-free skinny
- *     kernel, and the backward applies act' to dY as its GEMMs load it (none /
- *     ReLU / LeakyReLU) or, for GELU / Sigmoid / Tanh, which need dY' in a
- *     workspace, returns GEV2_MISSING_INPUT.
+ *     pass in `workspace`: the forward's split-K partial sums (skinny 16-bit
+ *     problems, and fp32 problems of at most 32 64x64 tiles with K >= 256;
+ *     gev2_gemm_fwd_workspace_size gives the size, 0 for all other problems)
+ *     and the backward's materialised dY'.  Such a buffer is allocated once
+ *     per (device, stream) and kept until gev2_stream_destroy.
+ *   - Nothing is allocated while `stream` is being captured into a HIP graph.
+ *     A per-stream buffer that an earlier eager call left large enough is
+ *     used (the graph then holds the same kernels as the eager call) and is
+ *     kept from then on until the process ends.  Without it, the forward uses
+ *     its scratch-free kernels, and the backward applies act' to dY as its
+ *     GEMMs load it (none / ReLU / LeakyReLU) or, for GELU / Sigmoid / Tanh,
+ *     which need dY' in a workspace, returns GEV2_MISSING_INPUT.
  */
 #ifndef GEV2_GEMM_H_
 #define GEV2_GEMM_H_

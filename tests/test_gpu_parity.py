@@ -359,6 +359,92 @@ def test_backward_both_dy_paths(gpu, fused, monkeypatch):
     assert_close(gb, ref["gBias"], 1.01 * M * U_ACC * aG.sum(0) + 1e-30, "gBias")
 
 
+SPLITK_CASES = [
+    # (M, N, K, act, bias): fp32 problems of at most 32 64x64 tiles with K >= 256 split K
+    (64, 256, 784, "relu", O.BIAS_PERN),      # C1
+    (100, 132, 1000, "gelu", O.BIAS_PERM),    # ragged M / N, K tail slice
+    (32, 64, 4096, "tanh", O.BIAS_SCALAR),    # one tile, many slices
+    (256, 512, 256, "none", O.BIAS_NONE),     # 32 tiles, the limit
+]
+
+
+@pytest.mark.parametrize("case", SPLITK_CASES, ids=lambda c: "x".join(map(str, c[:3])))
+def test_fp32_splitk(gpu, case, monkeypatch):
+    """fp32 split-K: slices on the tile kernel into fp32 partials, then an ordered sum with
+    alpha, bias, Z and act.  Within the fp32 bound of the oracle, bit-identical with or without
+    a caller workspace (same slices, same order), and equal to the unsplit path within the bound."""
+    capi = gpu
+    M, N, K, act, bk = case
+    path = _check_fwd(capi, M, N, K, F32, act, bk, seed=700 + M, alpha=0.5)
+    assert path == "tile:splitk", path
+    X, W, b = make_fwd_inputs(701, M, N, K, F32, bk)
+    dev = Dev(capi)
+    try:
+        pX, pW = dev.put(X), dev.put(W)
+        pb = dev.put(b) if b is not None else 0
+        kw = dict(dtype=F32, M=M, N=N, K=K, A=pX, B=pW, bias=pb, bias_kind=bk if b is not None else 0, act=act)
+        need = capi.fwd_workspace_size(Y=1 << 20, **kw)
+        assert need > 0
+        outs = []
+        for ws in (dev.empty(need), 0):
+            pY, pZ = dev.empty(M * N * 4), dev.empty(M * N * 4)
+            capi.gemm_fwd(Y=pY, Z=pZ, workspace=ws, workspace_bytes=need if ws else 0, **kw)
+            capi.synchronize()
+            outs.append((dev.get_f32(pY, (M, N)), dev.get_f32(pZ, (M, N))))
+        monkeypatch.setenv("GEV2_NO_SPLITK", "1")
+        pY, pZ = dev.empty(M * N * 4), dev.empty(M * N * 4)
+        capi.gemm_fwd(Y=pY, Z=pZ, **kw)
+        assert capi.last_path() != "tile:splitk"
+        capi.synchronize()
+        plain = dev.get_f32(pZ, (M, N))
+    finally:
+        dev.close()
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    bvals = O.bias_add(np.zeros((M, N)), b, bk) if b is not None else None
+    bz = fwd_bound(X, W, K, F32, bvals)
+    assert np.all(np.abs(plain - outs[0][1]) <= 2 * bz + 2 * U_OUT[F32] * np.abs(plain) + 1e-30)
+
+
+@pytest.mark.parametrize("case", [(64, 256, 784, "relu"), (100, 520, 132, "leakyrelu"), (40, 1000, 64, "none")],
+                         ids=lambda c: "x".join(map(str, c[:3])))
+def test_fp32_backward_dx_splitk(gpu, case, monkeypatch):
+    """Small fp32 backward with dY' formed while loading: dX (few 64x64 tiles, long reduction
+    over N) is split over workgroups into fp32 partials and summed in order.  Same result with
+    the caller's workspace as with the library's buffer, within the fp32 bound of the oracle,
+    and within twice that bound of the unsplit launch."""
+    capi = gpu
+    M, N, K, act = case
+    X, W, b = make_fwd_inputs(810 + M, M, N, K, F32, O.BIAS_PERN)
+    gY = np.random.default_rng(811 + M).standard_normal((M, N)).astype(np.float32)
+    Z = np.random.default_rng(812 + M).standard_normal((M, N)).astype(np.float32)
+    dev = Dev(capi)
+    try:
+        pX, pW, pgY, pZ = dev.put(X), dev.put(W), dev.put(gY), dev.put(Z)
+        kw = dict(dtype=F32, M=M, N=N, K=K, A=pX, B=pW, gY=pgY, Z=pZ, act=act, alpha=0.75)
+        import ctypes
+        need = capi.lib().gev2_gemm_bwd_workspace_size(ctypes.byref(capi.bwd_desc(gA=1 << 20, **kw)))
+        assert need > 0 and need % (M * K * 4) == 0 and need // (M * K * 4) >= 2   # >= 2 slices of [M,K] fp32
+        outs = []
+        for ws in (dev.empty(need), 0):
+            pgA = dev.empty(M * K * 4)
+            capi.gemm_bwd(gA=pgA, workspace=ws, workspace_bytes=need if ws else 0, **kw)
+            capi.synchronize()
+            outs.append(dev.get_f32(pgA, (M, K)))
+        monkeypatch.setenv("GEV2_NO_SPLITK", "1")
+        pgA = dev.empty(M * K * 4)
+        capi.gemm_bwd(gA=pgA, **kw)
+        capi.synchronize()
+        plain = dev.get_f32(pgA, (M, K))
+    finally:
+        dev.close()
+    assert np.array_equal(outs[0], outs[1])
+    ref = O.gemm_backward(X, W, gY, Z, act, 0.01, O.BIAS_NONE, 0.75)
+    aG = np.abs(gY.astype(np.float64) * O.act_deriv(Z, act))
+    bnd = 0.75 * 1.01 * N * U_ACC * (aG @ np.abs(W.astype(np.float64)).T) + U_OUT[F32] * np.abs(ref["gA"]) + 1e-30
+    assert_close(outs[0], ref["gA"], bnd, f"dX split {M}x{N}x{K}", rel_norm=1e-4)
+    assert np.all(np.abs(outs[0] - plain) <= 2 * bnd)
+
+
 def test_skinny_full_size(gpu):
     """BASELINE config 5b: M=8, N=K=4096, bf16, bias, through the skinny kernel."""
     path = _check_fwd(gpu, 8, 4096, 4096, BF16, "none", O.BIAS_PERN, seed=55)
