@@ -373,36 +373,41 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
 }
 
 // Y = act(alpha * sum_s part[s] + bias), K blocks added in order s = 0, 1, ...
-// One thread per (16-column tile, lane) of the MFMA result layout, i.e. per 4
-// rows of one column; up to 16 partial vectors are in flight at once.
+// One thread per (16-column tile, lane, row pair) of the MFMA result layout,
+// i.e. per 2 rows of one column, so that C5b's 2 MiB of partials spread over
+// 256 single-wave workgroups; every K block's partial is loaded at once.
 constexpr int kReduceThreads = 64;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 template <typename T>
 __global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArgs p, const f32x4_t* part, int nsplit,
                                                                        int ntile) {
   const int mq = (p.M + 3) / 4;
   const int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;
-  const int64_t per_split = (int64_t)ntile * 16 * mq;
-  if (i >= per_split) return;
-  const int tile = static_cast<int>(i / (16 * mq)), lane = static_cast<int>(i % (16 * mq));
-  f32x4_t sum = part[i];
-  for (int s0 = 1; s0 < nsplit; s0 += 16) {
-    f32x4_t v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      v[u] = s0 + u < nsplit ? part[(s0 + u) * per_split + i] : f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (s0 + u < nsplit)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sum[r] += v[u][r];
-  }
+  const int64_t per_split = (int64_t)ntile * 16 * mq;   // f32x4 vectors per K block
+  if (i >= 2 * per_split) return;
+  const int64_t v = i >> 1;
+  const int half = static_cast<int>(i & 1);
+  const int tile = static_cast<int>(v / (16 * mq)), lane = static_cast<int>(v % (16 * mq));
   const int n = tile * 16 + (lane & 15);
+  const int m0 = 4 * (lane >> 4) + 2 * half;
+  if (m0 >= p.M || n >= p.N) return;
+  const f32x2_t* src = reinterpret_cast<const f32x2_t*>(part) + 2 * v + half;
+  f32x2_t sum = src[0];
+  for (int s0 = 1; s0 < nsplit; s0 += 16) {
+    f32x2_t w[16];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * (lane >> 4) + r;
-    if (m < p.M && n < p.N) skinny_out<T>(p, m, n, sum[r]);
+    for (int u = 0; u < 16; ++u) w[u] = s0 + u < nsplit ? src[2 * (s0 + u) * per_split] : f32x2_t{0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (s0 + u < nsplit) {
+        sum[0] += w[u][0];
+        sum[1] += w[u][1];
+      }
   }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    if (m0 + r < p.M) skinny_out<T>(p, m0 + r, n, sum[r]);
 }
 
 template <typename T, int COLS>
@@ -415,7 +420,7 @@ static hipError_t launch_skinny_split_c(const SkinnyArgs& a, float* part, hipStr
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   const int ntile = nslab * (S::kCols / 16);
-  const int64_t threads = (int64_t)ntile * 16 * ((a.M + 3) / 4);
+  const int64_t threads = (int64_t)ntile * 16 * ((a.M + 3) / 4) * 2;
   hipLaunchKernelGGL((skinny_reduce_kernel<T>), dim3(static_cast<unsigned>((threads + kReduceThreads - 1) / kReduceThreads)),
                      dim3(kReduceThreads), 0, s, a, pv, nsplit, ntile);
   return hipGetLastError();
