@@ -52,7 +52,32 @@ struct AttnArgs {
   float scale;
   int causal;
   int qblocks;           // ceil(M / attn_wg_queries(QT))
+  int drop;              // dropout on (p > 0)
+  float drop_p;          // drop probability
+  float drop_scale;      // factor of a kept probability: 1/(1-p) when scale_in_train, else 1
+  uint64_t seed;         // dropout stream seed
 };
+
+// Dropout of the reference (dropout/kernels.cu:21-41): element (bh, q, key) of
+// the [B*H, M, N] probabilities is kept when u, the low 32 bits of
+// splitmix64(seed ^ counter) with counter = (bh*M + q)*N + key (the reference's
+// counter_base (b*H+h)*M*N plus the index in the slice, sdpa/launcher.cu:249-258),
+// gives float(u) * 2^-32 >= p.  splitmix64 is Steele, Lea and Flood's mixing
+// function (its standard constants, as in the reference).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  uint64_t z = x;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// The factor a probability is multiplied by: drop_scale if kept, else 0.
+__device__ __forceinline__ float drop_factor(const AttnArgs& a, int bh, int q, int key) {
+  const uint64_t ctr = ((uint64_t)bh * a.M + q) * a.N + key;
+  const uint32_t u = static_cast<uint32_t>(splitmix64(a.seed ^ ctr));
+  return static_cast<float>(u) * (1.0f / 4294967296.0f) >= a.drop_p ? a.drop_scale : 0.f;
+}
 
 // Mask term added to a scaled score (the reference adds the external mask,
 // then the causal term).
@@ -271,7 +296,12 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
           const float arg = MASKED ? x[kt][r] - m_new : fmaf(x[kt][r], xscale, -m_new);
           const float p = __builtin_amdgcn_exp2f(arg);
           lsum += p;
-          pb[kt][r] = Elem<T>::bits(p);
+          // dropout (masked variant only): the row sum keeps every probability,
+          // P V only the kept ones
+          if constexpr (MASKED)
+            pb[kt][r] = Elem<T>::bits(a.drop ? p * drop_factor(a, bh, q[qt], key0 + 16 * kt + r) : p);
+          else
+            pb[kt][r] = Elem<T>::bits(p);
         }
       }
       l_run[qt] = l_run[qt] * corr + lsum;
@@ -339,7 +369,7 @@ hipError_t launch_attn_fwd_qt(AttnArgs a, hipStream_t s) {
   constexpr int KT = D == 64 ? 8 : 4;       // 128 keys per block at D = 64 (two workgroups per CU fit in LDS)
   a.qblocks = (a.M + attn_wg_queries(QT) - 1) / attn_wg_queries(QT);
   const int64_t blocks = (int64_t)a.BH * a.qblocks;
-  if (a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f))
+  if (a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f) || a.drop)
     hipLaunchKernelGGL((attn_fwd_kernel<T, D, true, false, QT, KT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        s, a);
   else if (a.causal)
@@ -394,6 +424,17 @@ __global__ void __launch_bounds__(256) attn_softmax_rows_kernel(float* __restric
   for (int k = lane; k < a.N; k += 64) srow[k] *= inv;
 }
 
+// dst = dropout(P) over the [B*H, M, N] probabilities of the fp32 path
+// (dropout_run of launcher.cu:249-258 and 454-490); dst may be P itself.
+__global__ void __launch_bounds__(256) attn_dropout_kernel(const float* __restrict__ P, float* dst, AttnArgs a) {
+  const int64_t total = (int64_t)a.BH * a.M * a.N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / a.N;
+    const int key = static_cast<int>(i - row * a.N);
+    dst[i] = P[i] * drop_factor(a, static_cast<int>(row / a.M), static_cast<int>(row % a.M), key);
+  }
+}
+
 // dS = P * (dP - sum_k dP P) on unmasked positions, 0 where masked
 // (softmax_backward_run, then the mask / causal zeroing, launcher.cu:640-690).
 __global__ void __launch_bounds__(256) attn_softmax_bwd_rows_kernel(const float* __restrict__ P, float* __restrict__ dP,
@@ -405,6 +446,11 @@ __global__ void __launch_bounds__(256) attn_softmax_bwd_rows_kernel(const float*
   const int b = static_cast<int>(row / a.M) / a.H;
   const float* prow = P + row * a.N;
   float* grow = dP + row * a.N;
+  const int bh = static_cast<int>(row / a.M);
+  if (a.drop) {
+    // dP of the kept probabilities only (the reference's dropout backward, launcher.cu:566-590)
+    for (int k = lane; k < a.N; k += 64) grow[k] *= drop_factor(a, bh, q, k);
+  }
   float dot = 0.f;
   for (int k = lane; k < a.N; k += 64) dot += grow[k] * prow[k];
   for (int o = 32; o > 0; o >>= 1) dot = xor_sum(dot, o);
@@ -648,11 +694,15 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
         const float dq = dql[16 * t + 4 * g + r];
         float pv;
         if constexpr (MASKED) {
+          // dropout (masked variant only): dV takes the kept probabilities, dP
+          // the kept gradient (launcher.cu:454-590 regenerates the forward's mask)
           const bool in = key_ok && q_ok;
+          const float keep = a.drop && in ? drop_factor(a, bh, q, key) : 1.f;
           const float x = in ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : 0.f;
           pv = in ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
           const bool m = in ? masked_entry(a, b, q, key) : true;
-          ds[r] = m ? 0.f : pv * (pacc[r] - dq);
+          ds[r] = m ? 0.f : pv * (pacc[r] * keep - dq);
+          pv *= keep;
         } else {
           const bool live = key_ok && q_ok && !(a.causal && key > q);
           pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
@@ -785,10 +835,11 @@ attn_bwd_q_kernel(AttnBwdArgs ba) {
         const bool key_ok = key < a.N;
         if constexpr (MASKED) {
           const bool in = key_ok && q_ok;
+          const float dp = a.drop && in ? pacc[r] * drop_factor(a, bh, q, key) : pacc[r];
           const float x = in ? mask_add(sacc[r] * a.scale, a, b, q, key) * kLog2e : 0.f;
           const float pv = in ? __builtin_amdgcn_exp2f(x - lse2) : 0.f;
           const bool m = in ? masked_entry(a, b, q, key) : true;
-          ds[r] = m ? 0.f : pv * (pacc[r] - dq);
+          ds[r] = m ? 0.f : pv * (dp - dq);
         } else {
           const bool live = key_ok && q_ok && !(a.causal && key > q);
           const float pv = live ? __builtin_amdgcn_exp2f(fmaf(sacc[r], xscale, -lse2)) : 0.f;
@@ -827,7 +878,7 @@ hipError_t launch_attn_bwd(const AttnBwdArgs& ba, hipStream_t s) {
                      a.M, a.lse_ld);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const bool masked = a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f);
+  const bool masked = a.mask_kind != GEV2_MASK_NONE || !(a.scale > 0.f) || a.drop;
   if (ba.dK || ba.dV) {
     const dim3 grid(static_cast<unsigned>((int64_t)a.BH * ((a.N + 63) / 64)));
     // one LDS stage at D = 128 (3 waves per SIMD instead of 2: 582 -> 574 us at B 2, H 16,
@@ -917,7 +968,7 @@ int attn_check(const Desc* d, gev2::AttnArgs* a) {
   if (d->mask_kind < GEV2_MASK_NONE || d->mask_kind > GEV2_MASK_F32)
     return attn_fail(GEV2_INVALID_ARGUMENT, "bad mask kind");
   if (d->mask_kind != GEV2_MASK_NONE && !d->mask) return attn_fail(GEV2_MISSING_INPUT, "mask kind set, mask null");
-  if (d->dropout_p != 0.f) return attn_fail(GEV2_UNIMPLEMENTED, "dropout_p != 0 is not implemented");
+  if (!(d->dropout_p >= 0.f && d->dropout_p <= 1.f)) return attn_fail(GEV2_INVALID_ARGUMENT, "dropout_p must be in [0, 1]");
   const int64_t BH = (int64_t)d->B * d->H;
   if (BH * d->M * d->D > 0x7fffffffLL || BH * d->N * d->D > 0x7fffffffLL || (int64_t)d->M * d->N > 0x7fffffffLL ||
       BH > 65535)
@@ -928,6 +979,11 @@ int attn_check(const Desc* d, gev2::AttnArgs* a) {
   a->causal = d->causal ? 1 : 0;
   a->mask = d->mask;
   a->mask_kind = d->mask_kind;
+  a->drop = d->dropout_p > 0.f ? 1 : 0;
+  a->drop_p = d->dropout_p;
+  // dropout/kernels.cu:43-47: kept values scaled by 1/(1-p) when scale_in_train and 1-p > 0
+  a->drop_scale = (d->scale_in_train && (1.0f - d->dropout_p) > 0.f) ? 1.0f / (1.0f - d->dropout_p) : 1.0f;
+  a->seed = d->seed;
   return GEV2_OK;
 }
 
@@ -1018,6 +1074,11 @@ int gev2_sdpa_fwd(const gev2_sdpa_desc* d, void* stream) {
                      S, a);
   st = hip_status(hipGetLastError(), "softmax");
   if (st != GEV2_OK) return st;
+  if (a.drop) {
+    hipLaunchKernelGGL(gev2::attn_dropout_kernel, dim3(4096), dim3(256), 0, s, S, S, a);
+    st = hip_status(hipGetLastError(), "dropout");
+    if (st != GEV2_OK) return st;
+  }
   return slice_gemm(GEV2_F32, false, false, 1.f, a.BH, M, D, N, S, N, M * N, d->V, D, N * D, d->Y, D, M * D, stream);
 }
 
@@ -1100,9 +1161,16 @@ int gev2_sdpa_bwd(const gev2_sdpa_bwd_desc* d, void* stream) {
                      a);
   st = hip_status(hipGetLastError(), "softmax");
   if (st != GEV2_OK) return st;
-  // dV = P^T dY
+  // dV = P^T dY, with the dropped P (in the dP buffer, free until dP below) under dropout
   if (d->dV) {
-    st = slice_gemm(GEV2_F32, true, false, 1.f, BH, N, D, M, P, N, M * N, d->dY, D, M * D, d->dV, D, N * D, stream);
+    const float* Pv = P;
+    if (a.drop) {
+      hipLaunchKernelGGL(gev2::attn_dropout_kernel, dim3(4096), dim3(256), 0, s, P, dP, a);
+      st = hip_status(hipGetLastError(), "dropout");
+      if (st != GEV2_OK) return st;
+      Pv = dP;
+    }
+    st = slice_gemm(GEV2_F32, true, false, 1.f, BH, N, D, M, Pv, N, M * N, d->dY, D, M * D, d->dV, D, N * D, stream);
     if (st != GEV2_OK) return st;
   }
   if (!d->dQ && !d->dK) return GEV2_OK;

@@ -53,6 +53,8 @@ void fill(D& d, const Tensor& Q, const Tensor& K, const Tensor* mask, const SDPA
   d.scale = a.scale;
   d.causal = a.causal ? 1 : 0;
   d.dropout_p = a.dropout_p;
+  d.seed = a.seed;
+  d.scale_in_train = a.scale_in_train ? 1 : 0;
   d.mask_kind = mask_kind(mask);
   d.mask = mask ? mask->data : nullptr;
 }

@@ -8,8 +8,8 @@
 // the call; callers that cannot allocate use gev2_sdpa_fwd / gev2_sdpa_bwd with
 // a workspace instead.
 // Differences a caller can observe: F16 / BF16 tensors are accepted (with
-// D = 64 or 128 the forward and backward are fused kernels);
-// dropout_p > 0 returns Status::Unimplemented.
+// D = 64 or 128 the forward and backward are fused kernels, dropout
+// included).
 #pragma once
 #include <cstdint>
 

@@ -131,6 +131,7 @@ class SdpaDesc(ctypes.Structure):
     _fields_ = [
         *_SDPA_HEAD, ("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("Y", ctypes.c_void_p),
         ("lse", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("seed", ctypes.c_uint64), ("scale_in_train", ctypes.c_int32), ("reserved1", ctypes.c_int32),
     ]
 
 
@@ -138,7 +139,8 @@ class SdpaBwdDesc(ctypes.Structure):
     _fields_ = [
         *_SDPA_HEAD, ("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("dY", ctypes.c_void_p),
         ("dQ", ctypes.c_void_p), ("dK", ctypes.c_void_p), ("dV", ctypes.c_void_p), ("workspace", ctypes.c_void_p),
-        ("workspace_bytes", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_int64), ("seed", ctypes.c_uint64), ("scale_in_train", ctypes.c_int32),
+        ("reserved1", ctypes.c_int32),
     ]
 
 

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GEV2_ABI_VERSION 3
+#define GEV2_ABI_VERSION 4
 
 /* Status (values of ai::cuda::shim::Status, ai_status.hpp:14-43) */
 enum {
@@ -327,7 +327,13 @@ const char* gev2_rnn_last_error(void);
  * Q [B,H,M,D], K / V [B,H,N,D], Y [B,H,M,D], contiguous, one dtype.
  * scale 0 means 1/sqrt(D).  causal adds -1e9 where key > query; mask
  * [B,1,M,N] (broadcast over H): I8 / I32 entries != 0 add -1e9, F32 entries
- * are added.  dropout_p must be 0 (GEV2_UNIMPLEMENTED otherwise).
+ * are added.  Dropout (dropout_p in [0, 1]) follows the reference's
+ * stateless stream (dropout/kernels.cu:21-41, sdpa/launcher.cu:249-258,
+ * 454-470): probability (b, h, q, key) is kept when the low 32 bits u of
+ * splitmix64(seed ^ ((((b*H + h)*M + q)*N + key)) give float(u) * 2^-32 >= p,
+ * and kept ones are scaled by 1/(1 - p) when scale_in_train (and p < 1); the
+ * row sums of the softmax and the backward's regenerated mask use the same
+ * stream, so one (seed, p) pair gives the same mask in both.
  * Forward, F16 / BF16 with D = 64 or 128: one fused kernel, no workspace;
  * `lse` (optional, fp32 [B,H,M]) receives each row's log-sum-exp.
  * Forward, F32: S / P in `workspace` (gev2_sdpa_workspace_size bytes).
@@ -352,6 +358,9 @@ typedef struct gev2_sdpa_desc {
   void* Y;
   float* lse;
   void* workspace;  int64_t workspace_bytes;
+  uint64_t seed;                    /* dropout stream seed */
+  int32_t scale_in_train;           /* 1: kept probabilities scaled by 1/(1-p) */
+  int32_t reserved1;
 } gev2_sdpa_desc;
 
 /* dQ / dK / dV (each optional, not all NULL) of the forward above for dY. */
@@ -371,6 +380,9 @@ typedef struct gev2_sdpa_bwd_desc {
   void* dK;
   void* dV;
   void* workspace;  int64_t workspace_bytes;
+  uint64_t seed;
+  int32_t scale_in_train;
+  int32_t reserved1;
 } gev2_sdpa_bwd_desc;
 
 int gev2_sdpa_fwd(const gev2_sdpa_desc* desc, void* stream);

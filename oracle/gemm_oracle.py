@@ -30,7 +30,9 @@ It restates, in float64 NumPy, the host math of the reference:
   (S = scale Q K^T, scale 0 -> 1/sqrt(D); external mask [B,1,M,N] then causal,
   each adding -1e9 in fp32 (F32 masks add their value); softmax over keys;
   Y = P V; backward dV = P^T dY, dS = P (dP - rowsum(dP P)) zeroed where
-  masked, dQ = scale dS K, dK = scale dS^T Q)
+  masked, dQ = scale dS K, dK = scale dS^T Q; dropout with the stateless
+  splitmix64 stream of ``dropout/kernels.cu:8-45``, P dropped in Y = P V and
+  in dV, dP dropped before dS)
 * Elman RNN             -- ``backends/cuda/ops/rnn/launcher.cu:129-383``
   (h_t = act(X_t Wx + h_{t-1} Wh + b); backward through time with
   dh_next = dZ_t Wh^T; dB summed over all steps)
@@ -491,9 +493,38 @@ def _sdpa_scores(Q, K, scale, causal, mask, mask_kind):
     return out, np.broadcast_to(hit, S.shape)
 
 
-def sdpa_forward(Q, K, V, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE):
-    """Y = softmax(scale Q K^T + masks) V over [B,H,M,N] (launcher.cu:129-274).
-    Returns (Y, P, lse) in float64; lse = log sum exp of the masked scaled scores per row."""
+_U64 = np.uint64
+
+
+def splitmix64(x) -> np.ndarray:
+    """The reference's mixing function (dropout/kernels.cu:8-15; Steele, Lea and Flood's
+    SplitMix64 output step), on uint64 arrays with arithmetic modulo 2^64."""
+    with np.errstate(over="ignore"):
+        z = np.asarray(x, dtype=np.uint64) + _U64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> _U64(30))) * _U64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> _U64(27))) * _U64(0x94D049BB133111EB)
+        return z ^ (z >> _U64(31))
+
+
+def dropout_factors(seed: int, B: int, H: int, M: int, N: int, p: float, scale_in_train: bool = True) -> np.ndarray:
+    """The factor dropout multiplies each attention probability by, [B,H,M,N] float32:
+    kept -> 1/(1-p) (scale_in_train and 1-p > 0; else 1), dropped -> 0.  Element (b,h,q,k)
+    uses counter (b*H+h)*M*N + q*N + k (sdpa/launcher.cu:249-258) and is kept when the low 32
+    bits u of splitmix64(seed ^ counter) give float32(u) * 2^-32 >= p (dropout/kernels.cu:17-45)."""
+    ctr = np.arange(B * H * M * N, dtype=np.uint64)
+    u = (splitmix64(_U64(seed) ^ ctr) & _U64(0xFFFFFFFF)).astype(np.uint32)
+    r = u.astype(np.float32) * np.float32(1.0 / 4294967296.0)
+    keep = r >= np.float32(p)
+    one_m_p = np.float32(1.0) - np.float32(p)
+    s = np.float32(1.0) / one_m_p if (scale_in_train and one_m_p > 0) else np.float32(1.0)
+    return np.where(keep, s, np.float32(0)).astype(np.float32).reshape(B, H, M, N)
+
+
+def sdpa_forward(Q, K, V, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE,
+                 dropout_p: float = 0.0, seed: int = 0, scale_in_train: bool = True):
+    """Y = dropout(softmax(scale Q K^T + masks)) V over [B,H,M,N] (launcher.cu:129-274).
+    Returns (Y, P, lse) in float64, with P and lse those of the softmax before dropout;
+    lse = log sum exp of the masked scaled scores per row."""
     D = np.asarray(Q).shape[-1]
     sc = scale if scale != 0.0 else 1.0 / math.sqrt(D)
     S, _ = _sdpa_scores(Q, K, sc, causal, mask, mask_kind)
@@ -501,19 +532,26 @@ def sdpa_forward(Q, K, V, scale: float = 0.0, causal: bool = False, mask=None, m
     E = np.exp(S - mx)
     l = E.sum(axis=-1, keepdims=True)
     P = E / l
-    Y = np.einsum("bhmn,bhnd->bhmd", P, np.asarray(V, np.float64), optimize=True)
+    Pd = P
+    if dropout_p > 0:
+        Pd = P * dropout_factors(seed, *P.shape, dropout_p, scale_in_train)
+    Y = np.einsum("bhmn,bhnd->bhmd", Pd, np.asarray(V, np.float64), optimize=True)
     return Y, P, (mx + np.log(l))[..., 0]
 
 
-def sdpa_backward(Q, K, V, dY, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE):
-    """dQ, dK, dV of sdpa_forward for upstream dY (launcher.cu:333-747), float64."""
+def sdpa_backward(Q, K, V, dY, scale: float = 0.0, causal: bool = False, mask=None, mask_kind: int = MASK_NONE,
+                  dropout_p: float = 0.0, seed: int = 0, scale_in_train: bool = True):
+    """dQ, dK, dV of sdpa_forward for upstream dY (launcher.cu:333-747), float64.  With
+    dropout (launcher.cu:454-590): dV = dropout(P)^T dY, and dP = dropout-backward(dY V^T)
+    enters dS = P (dP - rowsum(dP P))."""
     Q, K, V, dY = (np.asarray(a, np.float64) for a in (Q, K, V, dY))
     D = Q.shape[-1]
     sc = scale if scale != 0.0 else 1.0 / math.sqrt(D)
     _, P, _ = sdpa_forward(Q, K, V, scale, causal, mask, mask_kind)
     _, hit = _sdpa_scores(Q, K, sc, causal, mask, mask_kind)
-    dV = np.einsum("bhmn,bhmd->bhnd", P, dY, optimize=True)
-    dP = np.einsum("bhmd,bhnd->bhmn", dY, V, optimize=True)
+    f = dropout_factors(seed, *P.shape, dropout_p, scale_in_train) if dropout_p > 0 else 1.0
+    dV = np.einsum("bhmn,bhmd->bhnd", P * f, dY, optimize=True)
+    dP = np.einsum("bhmd,bhnd->bhmn", dY, V, optimize=True) * f
     dS = P * (dP - (dP * P).sum(axis=-1, keepdims=True))
     dS = np.where(hit, 0.0, dS)
     dQ = sc * np.einsum("bhmn,bhnd->bhmd", dS, K, optimize=True)

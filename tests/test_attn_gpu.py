@@ -3,7 +3,9 @@ the sdpa op of sdpa/launcher.cu:129-747) against the float64 oracle:
   - the fused 16-bit kernel (bf16 / fp16, D = 64 and 128) with ragged M / N, causal and the
     three external mask kinds, and its row log-sum-exp;
   - the fp32 path (the reference's type) forward and backward, with the same masks;
-  - the reference's validation results (dropout, all-null outputs)."""
+  - dropout with the reference's stateless splitmix64 stream: the dropped set bit-exact
+    against the oracle, forward and backward within tolerance on both paths;
+  - the reference's validation results (dropout_p range, all-null outputs)."""
 import ctypes
 import math
 
@@ -35,7 +37,8 @@ def _mask(kind, B, M, N, seed):
     return np.where(hit, -2.5, 0.0).astype(np.float32)
 
 
-def _fwd(capi, Q, K, V, dtype, causal=False, mask=None, mask_kind=O.MASK_NONE, scale=0.0, want_lse=True):
+def _fwd(capi, Q, K, V, dtype, causal=False, mask=None, mask_kind=O.MASK_NONE, scale=0.0, want_lse=True,
+         dropout_p=0.0, seed=0, scale_in_train=True):
     B, H, M, D = Q.shape
     N = K.shape[2]
     bufs = [capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype)) for a in (Q, K, V)]
@@ -45,7 +48,8 @@ def _fwd(capi, Q, K, V, dtype, causal=False, mask=None, mask_kind=O.MASK_NONE, s
     mk = capi.DeviceBuffer.from_numpy(mask) if mask is not None else None
     d = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, scale=scale, causal=int(causal), mask_kind=mask_kind,
                       mask=mk.ptr if mk else None, Q=bufs[0].ptr, K=bufs[1].ptr, V=bufs[2].ptr, Y=Y.ptr,
-                      lse=lse.ptr if lse else None)
+                      lse=lse.ptr if lse else None, dropout_p=dropout_p, seed=seed,
+                      scale_in_train=int(scale_in_train))
     L = capi.lib()
     wsb = L.gev2_sdpa_workspace_size(ctypes.byref(d), 0)
     ws = capi.DeviceBuffer(max(wsb, 1)) if wsb > 0 else None
@@ -136,8 +140,10 @@ def test_f32_forward_backward(capi, causal, mk):
 
 def test_validation(capi):
     L = capi.lib()
-    d = capi.SdpaDesc(dtype=BF16, B=1, H=1, M=8, N=8, D=64, dropout_p=0.1, Q=16, K=32, V=48, Y=64)
-    assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 2            # Unimplemented (dropout)
+    d = capi.SdpaDesc(dtype=BF16, B=1, H=1, M=8, N=8, D=64, dropout_p=1.5, Q=16, K=32, V=48, Y=64)
+    assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 4            # dropout_p outside [0, 1]
+    d.dropout_p = -0.1
+    assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 4
     d.dropout_p, d.mask_kind = 0.0, O.MASK_I8
     assert L.gev2_sdpa_fwd(ctypes.byref(d), None) == 10           # mask kind without a mask
     b = capi.SdpaBwdDesc(dtype=F32, B=1, H=1, M=8, N=8, D=16, Q=16, K=32, V=48, dY=64)
@@ -242,3 +248,71 @@ def test_host_api(capi, host, dtype, causal, mk):
     assert np.abs(y.get() - Y64).max() <= tol * max(1.0, np.abs(Y64).max())
     for g_, r in ((gq, ref["dQ"]), (gk, ref["dK"]), (gv, ref["dV"])):
         assert np.abs(g_.get() - r).max() <= tol * max(1.0, np.abs(r).max())
+
+
+# ---------------------------------------------------------------------------
+# Dropout (the reference's stateless stream, dropout/kernels.cu:8-45)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,D", [(BF16, 64), (F16, 128), (F32, 64)], ids=["bf16-d64", "f16-d128", "f32-d64"])
+@pytest.mark.parametrize("scale_in_train", [True, False], ids=["scaled", "unscaled"])
+def test_dropout_mask_exact(capi, dtype, D, scale_in_train):
+    """Q = K = 0 make every probability 1/N, and V = I (N = D keys) makes Y = dropout(P) itself:
+    Y must equal factor / N bit for bit (1.25 / N and 1 / N are exact in every storage type),
+    so the kept set of every (b, h, query, key) is checked against the oracle's stream."""
+    B, H, M, N, p, seed = 2, 3, 96, D, 0.2, 20261202
+    Q = np.zeros((B, H, M, D), np.float32)
+    K = np.zeros((B, H, N, D), np.float32)
+    V = np.broadcast_to(np.eye(N, D, dtype=np.float32), (B, H, N, D)).copy()
+    y, _ = _fwd(capi, Q, K, V, dtype, want_lse=False, dropout_p=p, seed=seed, scale_in_train=scale_in_train)
+    f = O.dropout_factors(seed, B, H, M, N, p, scale_in_train)
+    assert np.array_equal(y != 0, f != 0), int(((y != 0) != (f != 0)).sum())
+    assert np.array_equal(y, (f / np.float32(N)).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype,D,causal", [(BF16, 64, False), (F16, 128, True), (F32, 32, False)],
+                         ids=["bf16-d64", "f16-d128-causal", "f32-d32"])
+def test_dropout_forward_backward(capi, dtype, D, causal, monkeypatch):
+    """Random inputs with dropout p = 0.3: the forward within the fused / fp32 bounds used above
+    (computed with the dropped probabilities), and dQ / dK / dV of the fused (16-bit) or batched
+    fp32 backward against the oracle's gradient of the same dropped function."""
+    B, H, M, N, p, seed = 1, 2, 130, 100, 0.3, 77
+    Q, K, V = _qkv(61, B, H, M, N, D, dtype)
+    y, lse = _fwd(capi, Q, K, V, dtype, causal, want_lse=dtype != F32, dropout_p=p, seed=seed)
+    Y64, P64, lse64 = O.sdpa_forward(Q, K, V, causal=causal, dropout_p=p, seed=seed)
+    Pd = P64 * O.dropout_factors(seed, B, H, M, N, p)
+    if dtype == F32:
+        np.testing.assert_allclose(y, Y64, rtol=1e-4, atol=1e-5)
+    else:
+        eps = O.storage_eps(dtype)
+        bound = 2 * eps * np.einsum("bhmn,bhnd->bhmd", Pd, np.abs(V)) + 1e-4 + eps * np.abs(Y64)
+        err = np.abs(y - Y64)
+        assert np.all(err <= bound), (float(err.max()), np.unravel_index(int(np.argmax(err - bound)), err.shape))
+        assert np.all(np.abs(lse - lse64) <= 1e-4 * (1 + np.abs(lse64)))   # lse of the undropped softmax
+    dY = rounded(np.random.default_rng(62).standard_normal(Q.shape), dtype).astype(np.float32)
+    bufs = [capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype)) for a in (Q, K, V, dY)]
+    es = capi.elem_bytes(dtype)
+    outs = [capi.DeviceBuffer(a.size * es) for a in (Q, K, V)]
+    L = capi.lib()
+    fd = capi.SdpaDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal), dropout_p=p, seed=seed,
+                       scale_in_train=1)
+    wsb = L.gev2_sdpa_workspace_size(ctypes.byref(fd), 1)
+    ws = capi.DeviceBuffer(wsb)
+    d = capi.SdpaBwdDesc(dtype=dtype, B=B, H=H, M=M, N=N, D=D, causal=int(causal), dropout_p=p, seed=seed,
+                         scale_in_train=1, Q=bufs[0].ptr, K=bufs[1].ptr, V=bufs[2].ptr, dY=bufs[3].ptr,
+                         dQ=outs[0].ptr, dK=outs[1].ptr, dV=outs[2].ptr, workspace=ws.ptr, workspace_bytes=wsb)
+    capi.check_sdpa(L.gev2_sdpa_bwd(ctypes.byref(d), None), "sdpa bwd dropout")
+    capi.synchronize()
+    ref = O.sdpa_backward(Q, K, V, dY, causal=causal, dropout_p=p, seed=seed)
+    st = capi.to_storage(np.zeros(1, np.float32), dtype).dtype
+    dq_term = (np.abs(dY) * np.abs(Y64)).sum(-1).max() / np.sqrt(D)
+    t = {"dQ": dq_term * np.abs(K).max(), "dK": dq_term * np.abs(Q).max(), "dV": 0.0}
+    for name, buf, a in zip(("dQ", "dK", "dV"), outs, (Q, K, V)):
+        g = capi.from_storage(buf.download(a.shape, st), dtype)
+        r = ref[name]
+        if dtype == F32:
+            np.testing.assert_allclose(g, r, rtol=1e-4, atol=1e-4, err_msg=name)
+        else:
+            eps = O.storage_eps(dtype)
+            err = float(np.abs(g - r).max())
+            # the dropped P enters dV as a 16-bit value scaled by 1/(1-p): one more factor of it
+            assert err <= 8 * eps * (np.abs(r).max() + t[name]) / (1 - p), (name, err, float(np.abs(r).max()))

@@ -26,7 +26,7 @@ def test_exports_every_declared_symbol(capi):
     missing = [n for n in sorted(names) if not hasattr(L, n)]
     assert not missing, missing
     assert set(names) <= set(capi.EXPORTED)
-    assert L.gev2_abi_version() == 3
+    assert L.gev2_abi_version() == 4
 
 
 def test_status_strings(capi):

@@ -560,3 +560,76 @@ def test_sdpa_backward_matches_finite_difference(causal, mk):
             m[k][idx] -= h
             fd = (loss(*p) - loss(*m)) / (2 * h)
             assert abs(fd - r[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (name, idx, fd, r[name][idx])
+
+
+# ---------------------------------------------------------------------------
+# Attention dropout: the reference's stateless splitmix64 stream
+# ---------------------------------------------------------------------------
+def test_splitmix64_known_answers():
+    """SplitMix64's published output sequences (Vigna's reference splitmix64.c): the n-th
+    output of a generator seeded with s is the mixing function applied to s + (n-1)*gamma,
+    i.e. splitmix64(s + (n-1)*gamma) here (the function adds gamma itself)."""
+    gamma = 0x9E3779B97F4A7C15
+    M64 = (1 << 64) - 1
+    seq = {0: [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F],
+           1234567: [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+                     16408922859458223821]}
+    for seed, outs in seq.items():
+        x = np.array([(seed + i * gamma) & M64 for i in range(len(outs))], np.uint64)
+        assert [int(v) for v in O.splitmix64(x)] == outs
+
+
+def test_dropout_factors_stream():
+    """Counter layout, keep rule and scaling: element (b,h,q,k) uses counter ((b*H+h)*M+q)*N+k;
+    p = 0 keeps everything unscaled; the kept fraction matches 1 - p within 5 sigma; kept
+    entries carry 1/(1-p) (or 1 without scale_in_train); p = 1 drops everything."""
+    B, H, M, N, seed = 2, 3, 40, 50, 987654321
+    f = O.dropout_factors(seed, B, H, M, N, 0.25)
+    # one element recomputed with Python integers from the counter formula
+    b, h, q, k = 1, 2, 17, 33
+    ctr = ((b * H + h) * M + q) * N + k
+    u = int(O.splitmix64(np.array([seed ^ ctr], np.uint64))[0]) & 0xFFFFFFFF
+    kept = float(np.float32(u)) * 2.0 ** -32 >= 0.25
+    assert f[b, h, q, k] == (np.float32(1) / np.float32(0.75) if kept else 0)
+    n = f.size
+    frac = float((f > 0).mean())
+    assert abs(frac - 0.75) <= 5 * math.sqrt(0.75 * 0.25 / n)
+    assert set(np.unique(f)) <= {0.0, float(np.float32(1) / np.float32(0.75))}
+    assert np.all(O.dropout_factors(seed, B, H, M, N, 0.0) == 1)
+    g = O.dropout_factors(seed, B, H, M, N, 0.25, scale_in_train=False)
+    assert np.array_equal(g > 0, f > 0) and set(np.unique(g)) <= {0.0, 1.0}
+    assert np.all(O.dropout_factors(seed, B, H, M, N, 1.0) == 0)
+    # another seed gives another mask
+    assert not np.array_equal(O.dropout_factors(seed + 1, B, H, M, N, 0.25) > 0, f > 0)
+
+
+def test_sdpa_dropout_forward_and_backward():
+    """With dropout, Y = (P . factors) V (so Q = K = 0 and V = I expose the factors directly),
+    and the backward is the gradient of that function for the fixed mask (central finite
+    differences of a scalar loss)."""
+    B, H, M, N = 2, 2, 5, 7
+    seed, p = 42, 0.3
+    Y, _, _ = O.sdpa_forward(np.zeros((B, H, M, N)), np.zeros((B, H, N, N)), np.broadcast_to(np.eye(N), (B, H, N, N)),
+                             dropout_p=p, seed=seed)
+    assert np.allclose(Y, O.dropout_factors(seed, B, H, M, N, p) / N, atol=1e-15)
+    Q, K, V = _qkv(56)
+    dY = np.random.default_rng(4).standard_normal(Q.shape)
+    r = O.sdpa_backward(Q, K, V, dY, dropout_p=p, seed=seed)
+
+    def loss(Q_, K_, V_):
+        return float((dY * O.sdpa_forward(Q_, K_, V_, dropout_p=p, seed=seed)[0]).sum())
+
+    args = [Q, K, V]
+    h = 1e-6
+    for k, name, idxs in ((0, "dQ", [(0, 1, 2, 3), (1, 0, 4, 0)]), (1, "dK", [(0, 0, 6, 1), (1, 1, 2, 2)]),
+                          (2, "dV", [(1, 0, 3, 3), (0, 1, 0, 0)])):
+        for idx in idxs:
+            a_, m_ = [a.copy() for a in args], [a.copy() for a in args]
+            a_[k][idx] += h
+            m_[k][idx] -= h
+            fd = (loss(*a_) - loss(*m_)) / (2 * h)
+            assert abs(fd - r[name][idx]) <= 1e-5 * max(1.0, abs(fd)), (name, idx, fd, r[name][idx])
+    # p = 0 is the plain attention
+    r0 = O.sdpa_backward(Q, K, V, dY)
+    rz = O.sdpa_backward(Q, K, V, dY, dropout_p=0.0, seed=seed)
+    assert all(np.array_equal(r0[k], rz[k]) for k in r0)

@@ -24,8 +24,8 @@ def test_validation(sd):
     with pytest.raises(RuntimeError, match="Status=103"):
         sd.forward(16, q, 32, q, 48, [2, 2, 9, 64], 64, q)                           # V.N != K.N
     a = sd.SDPAAttrs()
-    a.dropout_p = 0.1
-    with pytest.raises(RuntimeError, match="Status=2"):                             # dropout: Unimplemented
+    a.dropout_p = 1.5
+    with pytest.raises(RuntimeError, match="Status=4"):                             # dropout_p outside [0, 1]
         sd.forward(16, q, 32, q, 48, q, 64, q, attrs=a, dtype=sd.DType.BF16)
     with pytest.raises(ValueError, match="4D"):
         sd.forward(16, [2, 8, 64], 32, q, 48, q, 64, q)
