@@ -676,6 +676,11 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       pa.sPartial = static_cast<int64_t>(row_blocks) * N;
       pa.M = static_cast<int>(M); pa.N = static_cast<int>(N);
       pa.act = d->act; pa.slope = d->leaky_slope;
+      if (want_bias && d->bias_kind == GEV2_BIAS_PER_M) {
+        // row sums of dY' are the PerM bias gradient
+        pa.rowsum = d->gBias; pa.sRowsum = d->stride_gbias;
+        bias_done = true;
+      }
       e = gev2::launch_grad_prep(dt, pa, batch, s);
       if (e != hipSuccess) return hip_fail(e, "gZ launch");
       if (sums) {

@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "../../include/gev2_gemm.h"
 #include "gev2_device.hpp"
@@ -203,23 +204,167 @@ __global__ void __launch_bounds__(256) col2im_t_kernel(const T* __restrict__ dco
   store_run(reinterpret_cast<U*>(dXt) + row * g.W + w0, v, g.W - w0, vec != 0);
 }
 
-// acc[i] = (first ? 0 : acc[i]) + src[0*n + i] + src[1*n + i] + ... (slices in order)
+// col2im_t for unit horizontal stride with 16-byte aligned dcol rows (HWo a
+// multiple of the chunk): a thread's kRun outputs read kRun consecutive
+// elements of each contributing dcol row, at an offset that is not chunk
+// aligned.  The thread loads the aligned 16-byte chunks that cover that window
+// and shifts it into place in registers, instead of kRun element loads.
+// Chunks that would lie outside the dcol row are clamped into it: they can
+// only hold elements whose output position is masked.  Sums are formed in the
+// same (kh, kw) order as col2im_t_kernel, so the two give identical results.
 template <typename T>
-__global__ void __launch_bounds__(256) acc_add_kernel(float* __restrict__ acc, const T* __restrict__ src, int64_t n,
-                                                      int slices, int first) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  float v = first ? 0.f : acc[i];
-  // the loads run ahead of the adds, which keep the slice order
+__global__ void __launch_bounds__(256) col2im_vec_kernel(const T* __restrict__ dcol, T* __restrict__ dXt, ConvGeom g,
+                                                         int runs_per_row, int64_t threads, int vec) {
+  using U = typename Word<T>::type;
+  constexpr int EPC = Elem<T>::kPerChunk;        // elements per chunk
+  constexpr int EW = 4 / sizeof(T);              // elements per 32-bit word
+  constexpr int NCH = kRun / EPC + 1;            // chunks covering a window
+  constexpr int NWD = 4 * NCH;                   // their words
+  constexpr int OUTW = kRun / EW;                // words of the window
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= threads) return;
+  const int64_t row = t / runs_per_row;             // (img*Cin + c)*H + h
+  const int w0 = static_cast<int>(t - row * runs_per_row) * kRun;
+  const int h = static_cast<int>(row % g.H);
+  const int64_t ic = row / g.H;                     // img*Cin + c
+  const int img = static_cast<int>(ic / g.Cin), c = static_cast<int>(ic - (int64_t)img * g.Cin);
+  const int HWo = g.Ho * g.Wo;
+  const int K = g.Cin * g.Kh * g.Kw;
+  const int row_chunks = HWo / EPC;
+  const T* __restrict__ base = dcol + ((int64_t)img * K + (int64_t)c * g.Kh * g.Kw) * HWo;
+  float acc[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) acc[j] = 0.f;
+  for (int kh = 0; kh < g.Kh; ++kh) {
+    const int hn = h + g.ph - kh * g.dh;
+    if (hn < 0) break;                              // hn only falls as kh grows
+    const int ho = hn / g.sh;
+    if (ho * g.sh != hn || ho >= g.Ho) continue;
+    const T* __restrict__ krow = base + (int64_t)kh * g.Kw * HWo;
+    for (int kw = 0; kw < g.Kw; ++kw) {
+      const int wn0 = w0 + g.pw - kw * g.dw;        // output column of the first output
+      const int a = ho * g.Wo + wn0;                // window start in the dcol row (may be < 0)
+      const int c0 = (a >= 0 ? a : a - (EPC - 1)) / EPC;
+      const int sh = a - c0 * EPC;                  // 0 .. EPC-1
+      const T* __restrict__ p = krow + (int64_t)kw * HWo;
+      uint32_t wd[NWD];
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) {
+        const int ci = min(max(c0 + q, 0), row_chunks - 1);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p + (int64_t)ci * EPC);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wd[4 * q + i] = v[i];
+      }
+      // shift left by sh / EW words (two select stages), then by the odd
+      // element of a 16-bit pair
+      const int bw = sh / EW;
+      if (bw & 1) {
+#pragma unroll
+        for (int i = 0; i + 1 < NWD; ++i) wd[i] = wd[i + 1];
+      }
+      if (bw & 2) {
+#pragma unroll
+        for (int i = 0; i + 2 < NWD; ++i) wd[i] = wd[i + 2];
+      }
+      uint32_t ow[OUTW];
+#pragma unroll
+      for (int q = 0; q < OUTW; ++q) {
+        if constexpr (EW == 2) ow[q] = (sh & 1) ? __builtin_amdgcn_alignbit(wd[q + 1], wd[q], 16) : wd[q];
+        else ow[q] = wd[q];
+      }
+#pragma unroll
+      for (int j = 0; j < kRun; ++j) {
+        const int wn = wn0 + j;
+        if (w0 + j < g.W && wn >= 0 && wn < g.Wo) {
+          if constexpr (EW == 2) acc[j] += Elem<T>::from_bits((ow[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+          else acc[j] += __uint_as_float(ow[j]);
+        }
+      }
+    }
+  }
+  U v[kRun];
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) v[j] = static_cast<U>(Elem<T>::bits(acc[j]));
+  store_run(reinterpret_cast<U*>(dXt) + row * g.W + w0, v, g.W - w0, vec != 0);
+}
+
+// Running sums over images, in fp32: acc[i] = (first ? 0 : acc[i]) + src[0*n + i]
+// + src[1*n + i] + ... with the slices added in order, so the sum does not depend
+// on how many images one call holds.  One launch serves two jobs, dW (slices of
+// T) and dB (fp32 slices).  A thread owns kAccV consecutive elements; with `vec`
+// (n a multiple of kAccV, both arrays 16-byte aligned) a slice is one 8- or
+// 16-byte load, and the loads of up to kAccSlices slices are issued before
+// their adds.
+constexpr int kAccV = 4;
+constexpr int kAccSlices = 16;
+
+struct AccJob {
+  float* acc; const void* src; int64_t n; int64_t threads; int vec;
+};
+
+template <typename T>
+__device__ __forceinline__ void acc_job(const AccJob& j, int64_t t, int slices, int first) {
+  using Raw = typename std::conditional<sizeof(T) == 2, u32x2, u32x4>::type;
+  const int64_t i0 = t * kAccV;
+  const T* __restrict__ src = static_cast<const T*>(j.src);
+  float v[kAccV];
+  if (j.vec) {
+    if (first) {
+#pragma unroll
+      for (int e = 0; e < kAccV; ++e) v[e] = 0.f;
+    } else {
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(j.acc + i0);
+#pragma unroll
+      for (int e = 0; e < kAccV; ++e) v[e] = a[e];
+    }
+    for (int s0 = 0; s0 < slices; s0 += kAccSlices) {
+      Raw r[kAccSlices];
+#pragma unroll
+      for (int u = 0; u < kAccSlices; ++u)
+        if (s0 + u < slices) r[u] = *reinterpret_cast<const Raw*>(src + (int64_t)(s0 + u) * j.n + i0);
+#pragma unroll
+      for (int u = 0; u < kAccSlices; ++u) {
+        if (s0 + u >= slices) break;
+#pragma unroll
+        for (int e = 0; e < kAccV; ++e) {
+          if constexpr (sizeof(T) == 2) v[e] += Elem<T>::from_bits((r[u][e >> 1] >> (16 * (e & 1))) & 0xffffu);
+          else v[e] += __uint_as_float(r[u][e]);
+        }
+      }
+    }
+    f32x4_t a;
+#pragma unroll
+    for (int e = 0; e < kAccV; ++e) a[e] = v[e];
+    *reinterpret_cast<f32x4_t*>(j.acc + i0) = a;
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < kAccV; ++e) {
+    const int64_t i = i0 + e;
+    if (i >= j.n) break;
+    float x = first ? 0.f : j.acc[i];
 #pragma unroll 8
-  for (int j = 0; j < slices; ++j) v += Elem<T>::load1(src + (int64_t)j * n + i);
-  acc[i] = v;
+    for (int q = 0; q < slices; ++q) x += Elem<T>::load1(src + (int64_t)q * j.n + i);
+    j.acc[i] = x;
+  }
 }
 
 template <typename T>
-__global__ void __launch_bounds__(256) acc_store_kernel(T* __restrict__ dst, const float* __restrict__ acc, int64_t n) {
+__global__ void __launch_bounds__(64) acc_add_kernel(AccJob w, AccJob b, int slices, int first) {
+  const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (t < w.threads) acc_job<T>(w, t, slices, first);
+  else if (t - w.threads < b.threads) acc_job<float>(b, t - w.threads, slices, first);
+}
+
+// The results: dW (rounded to T) from its sum and dB (fp32) from its sum, in
+// one launch.
+template <typename T>
+__global__ void __launch_bounds__(256) acc_store_kernel(T* __restrict__ dW, const float* __restrict__ accW, int64_t nW,
+                                                        float* __restrict__ dB, const float* __restrict__ accB,
+                                                        int64_t nB) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) Elem<T>::store1(dst + i, acc[i]);
+  if (i < nW) Elem<T>::store1(dW + i, accW[i]);
+  else if (i - nW < nB) dB[i - nW] = accB[i - nW];
 }
 
 constexpr int kIm2colLdsBytes = 32 * 1024;
@@ -260,22 +405,49 @@ static hipError_t launch_col2im(const void* dcol, void* dX, const ConvGeom& g, i
   const int64_t threads = (int64_t)imgs * g.Cin * g.H * runs;
   if ((threads + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
   const int vec = ((int64_t)g.W * sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(dX) % 16 == 0;
-  hipLaunchKernelGGL((col2im_t_kernel<T>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const T*>(dcol), static_cast<T*>(dX), g, runs, threads, vec);
+  const bool rows16 = ((int64_t)g.Ho * g.Wo * sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(dcol) % 16 == 0;
+  if (g.sw == 1 && rows16)
+    hipLaunchKernelGGL((col2im_vec_kernel<T>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const T*>(dcol), static_cast<T*>(dX), g, runs, threads, vec);
+  else
+    hipLaunchKernelGGL((col2im_t_kernel<T>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const T*>(dcol), static_cast<T*>(dX), g, runs, threads, vec);
+  return hipGetLastError();
+}
+
+inline AccJob acc_job_of(float* acc, const void* src, int64_t n, size_t es) {
+  AccJob j{acc, src, acc ? n : 0, 0, 0};
+  if (!acc) return j;
+  j.threads = (n + kAccV - 1) / kAccV;
+  j.vec = n % kAccV == 0 && reinterpret_cast<uintptr_t>(acc) % 16 == 0 &&
+          reinterpret_cast<uintptr_t>(src) % (kAccV * es) == 0;
+  return j;
+}
+
+// accW += the `slices` dW slices of T at gw (when accW is set), accB += the dB
+// slices at gb (when accB is set), in one launch.
+template <typename T>
+static hipError_t launch_acc_add(float* accW, const void* gw, int64_t nW, float* accB, const float* gb, int64_t nB,
+                                 int slices, bool first, hipStream_t s) {
+  const AccJob w = acc_job_of(accW, gw, nW, sizeof(T)), b = acc_job_of(accB, gb, nB, sizeof(float));
+  const int64_t threads = w.threads + b.threads;
+  if (threads == 0) return hipSuccess;
+  if ((threads + 63) / 64 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((acc_add_kernel<T>), dim3(static_cast<unsigned>((threads + 63) / 64)), dim3(64), 0, s, w, b,
+                     slices, first ? 1 : 0);
   return hipGetLastError();
 }
 
 template <typename T>
-static hipError_t launch_acc_add(float* acc, const void* src, int64_t n, int slices, bool first, hipStream_t s) {
-  hipLaunchKernelGGL((acc_add_kernel<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, acc,
-                     static_cast<const T*>(src), n, slices, first ? 1 : 0);
-  return hipGetLastError();
-}
-
-template <typename T>
-static hipError_t launch_acc_store(void* dst, const float* acc, int64_t n, hipStream_t s) {
+static hipError_t launch_acc_store(void* dW, const float* accW, int64_t nW, float* dB, const float* accB, int64_t nB,
+                                   hipStream_t s) {
+  if (!dW) nW = 0;
+  if (!dB) nB = 0;
+  const int64_t n = nW + nB;
+  if (n == 0) return hipSuccess;
+  if ((n + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((acc_store_kernel<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                     static_cast<T*>(dst), acc, n);
+                     static_cast<T*>(dW), accW, nW, dB, accB, nB);
   return hipGetLastError();
 }
 
@@ -434,12 +606,10 @@ int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* d, void* stream) {
     b.workspace = d->dz; b.workspace_bytes = d->dz_bytes;
     st = gemm_status(gev2_gemm_bwd(&b, stream));
     if (st != GEV2_OK) return st;
-    if (d->dW) {
-      st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_add, accW, d->gw, CK, c, n0 == 0, s), "acc dW");
-      if (st != GEV2_OK) return st;
-    }
-    if (d->dB) {
-      st = hip_status(gev2::launch_acc_add<float>(accB, gb, d->Cout, c, n0 == 0, s), "acc dB");
+    if (d->dW || d->dB) {
+      st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_add, d->dW ? accW : nullptr, d->gw, CK,
+                                      d->dB ? accB : nullptr, gb, d->Cout, c, n0 == 0, s),
+                      "acc dW / dB");
       if (st != GEV2_OK) return st;
     }
     if (d->dX) {
@@ -448,15 +618,8 @@ int gev2_conv2d_bwd(const gev2_conv2d_bwd_desc* d, void* stream) {
       if (st != GEV2_OK) return st;
     }
   }
-  if (d->dW) {
-    st = hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_store, d->dW, accW, CK, s), "store dW");
-    if (st != GEV2_OK) return st;
-  }
-  if (d->dB) {
-    st = hip_status(hipMemcpyAsync(d->dB, accB, sizeof(float) * d->Cout, hipMemcpyDeviceToDevice, s), "store dB");
-    if (st != GEV2_OK) return st;
-  }
-  return GEV2_OK;
+  return hip_status(GEV2_DISPATCH_T(d->dtype, gev2::launch_acc_store, d->dW, accW, CK, d->dB, accB, d->Cout, s),
+                    "store dW / dB");
 }
 
 }  // extern "C"

@@ -162,6 +162,54 @@ __global__ void __launch_bounds__(256) grad_prep_kernel(PrepArgs p) {
   }
 }
 
+// grad_prep for a PerM bias: one wave per row writes that row of dY' and its
+// sum, so the bias gradient needs no second pass over dY and Z.  Lanes take
+// chunks lane, lane + 64, ... (four per round, their loads issued together)
+// and add them in that order; the wave's butterfly then adds the lanes.
+template <typename T>
+__global__ void __launch_bounds__(256) grad_prep_rows_kernel(PrepArgs p) {
+  constexpr int EPC = Elem<T>::kPerChunk;
+  constexpr int U = 4;
+  const int bz = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= p.M) return;                              // wave-uniform; no barrier below
+  const T* grow = reinterpret_cast<const T*>(p.gY) + (int64_t)bz * p.sgY + (int64_t)m * p.ldgy;
+  const T* zrow = reinterpret_cast<const T*>(p.Z) + (int64_t)bz * p.sZ + (int64_t)m * p.ldz;
+  T* orow = reinterpret_cast<T*>(p.out) + (int64_t)bz * p.sOut + (int64_t)m * p.N;
+  float s = 0.f;
+  dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+    for (int n0 = lane * EPC; n0 < p.N; n0 += U * 64 * EPC) {
+      u32x4 g[U], z[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int n = n0 + u * 64 * EPC;
+        if (n < p.N) {
+          g[u] = *reinterpret_cast<const u32x4*>(grow + n);
+          z[u] = *reinterpret_cast<const u32x4*>(zrow + n);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int n = n0 + u * 64 * EPC;
+        if (n < p.N) {
+          float gv[EPC], zv[EPC];
+          chunk_to_f32<T>(g[u], gv);
+          chunk_to_f32<T>(z[u], zv);
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            gv[e] *= act_grad_t<ACT>(zv[e], p.slope);
+            s += gv[e];
+          }
+          *reinterpret_cast<u32x4*>(orow + n) = f32_to_chunk<T>(gv);
+        }
+      }
+    }
+  });
+  s = wave_sum(s);
+  if (lane == 0) p.rowsum[(int64_t)bz * p.sRowsum + m] = s;
+}
+
 // 64 columns x 4 row-block lanes per workgroup: lane g adds row blocks
 // g, g+4, ... in order (independent loads, unrolled), then the 4 lanes are
 // added in order.
@@ -274,6 +322,10 @@ hipError_t launch_splitk_reduce(const SplitkReduceArgs& a, hipStream_t s) {
 
 template <typename T>
 static hipError_t grad_prep_t(const PrepArgs& a, int batch, hipStream_t s) {
+  if (a.rowsum) {
+    hipLaunchKernelGGL(grad_prep_rows_kernel<T>, dim3((a.M + 3) / 4, batch), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   constexpr int COLS = 32 * Elem<T>::kPerChunk;
   dim3 grid((a.N + COLS - 1) / COLS, (a.M + kPrepRows - 1) / kPrepRows, batch);
   hipLaunchKernelGGL(grad_prep_kernel<T>, grid, dim3(256), 0, s, a);

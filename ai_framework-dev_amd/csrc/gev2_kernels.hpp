@@ -63,6 +63,8 @@ struct GradArgs {
 // N a multiple of the chunk, rows 16-byte aligned) plus, when `partial` is
 // set, fixed-order column sums per block of kPrepRows rows: partial[rb][n].
 // finish_col_sums adds the row-block partials of each column in order.
+// With `rowsum` set instead (a PerM bias), one wave forms each whole row and
+// writes its fixed-order sum to rowsum[batch * sRowsum + m].
 constexpr int kPrepRows = 64;
 struct PrepArgs {
   const void* gY; const void* Z; void* out; float* partial;
@@ -70,6 +72,7 @@ struct PrepArgs {
   int64_t sgY, sZ, sOut, sPartial;
   int M, N;
   int act; float slope;
+  float* rowsum; int64_t sRowsum;
 };
 hipError_t launch_grad_prep(int dtype, const PrepArgs& a, int batch, hipStream_t s);
 
