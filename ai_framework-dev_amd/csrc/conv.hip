@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(256) im2col_t_kernel(const T* __restrict__ Xt,
 // rows the band needs into LDS once (rows outside the image as zeros), then
 // writes the Kh*Kw col rows of the band as runs of kRun consecutive hw, so X
 // is read from HBM once instead of Kh*Kw times through the caches.
-template <typename T>
+template <typename T, bool WIN>
 __global__ void __launch_bounds__(256) im2col_lds_kernel(const T* __restrict__ Xt, T* __restrict__ colt, ConvGeom g,
                                                          int TH, int bands, int vec, int xvec) {
   using U = typename Word<T>::type;
@@ -143,6 +143,58 @@ __global__ void __launch_bounds__(256) im2col_lds_kernel(const T* __restrict__ X
   const int n_out = rows * g.Wo;
   const int runs = (n_out + kRun - 1) / kRun;
   U* __restrict__ col = reinterpret_cast<U*>(colt) + ((int64_t)img * K + (int64_t)c * KK) * HWo + ho0 * g.Wo;
+  if constexpr (WIN) {
+    // unit horizontal stride, Wo a multiple of kRun, 16-byte LDS rows: a run's
+    // kRun inputs are consecutive in one LDS row, read as the aligned chunks
+    // that cover them and shifted into place (chunks past either end of the
+    // band are clamped into it; they only feed masked positions)
+    constexpr int EPC = 16 / sizeof(U), EW = 4 / sizeof(U);
+    constexpr int NCH = kRun / EPC + 1, NWD = 4 * NCH, OUTW = kRun / EW;
+    const int lds_chunks = R * g.W / EPC;
+    const int rpr = g.Wo / kRun;                   // runs per output row
+    for (int run = threadIdx.x; run < KK * runs; run += 256) {
+      const int kidx = run / runs;
+      const int r0 = run - kidx * runs;
+      const int kh = kidx / g.Kw, kw = kidx - kh * g.Kw;
+      const int hl = r0 / rpr, wo0 = (r0 - hl * rpr) * kRun;
+      const int wi0 = wo0 + kw * g.dw - g.pw;
+      const int a = (hl * g.sh + kh * g.dh) * g.W + wi0;
+      const int c0 = (a >= 0 ? a : a - (EPC - 1)) / EPC;
+      const int sh = a - c0 * EPC;
+      uint32_t wd[NWD];
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) {
+        const int ci = min(max(c0 + q, 0), lds_chunks - 1);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(lds + ci * EPC);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wd[4 * q + i] = v[i];
+      }
+      const int bw = sh / EW;
+      if (bw & 1) {
+#pragma unroll
+        for (int i = 0; i + 1 < NWD; ++i) wd[i] = wd[i + 1];
+      }
+      if (bw & 2) {
+#pragma unroll
+        for (int i = 0; i + 2 < NWD; ++i) wd[i] = wd[i + 2];
+      }
+      U v[kRun];
+#pragma unroll
+      for (int q = 0; q < OUTW; ++q) {
+        uint32_t w;
+        if constexpr (EW == 2) w = (sh & 1) ? __builtin_amdgcn_alignbit(wd[q + 1], wd[q], 16) : wd[q];
+        else w = wd[q];
+#pragma unroll
+        for (int e = 0; e < EW; ++e) {
+          const int j = q * EW + e;
+          const bool in = static_cast<unsigned>(wi0 + j) < static_cast<unsigned>(g.W);
+          v[j] = in ? static_cast<U>(EW == 2 ? (w >> (16 * e)) & 0xffffu : w) : U(0);
+        }
+      }
+      store_run(col + (int64_t)kidx * HWo + hl * g.Wo + wo0, v, kRun, vec != 0);
+    }
+    return;
+  }
   for (int run = threadIdx.x; run < KK * runs; run += 256) {
     const int kidx = run / runs;
     const int o0 = (run - kidx * runs) * kRun;
@@ -324,7 +376,7 @@ __device__ __forceinline__ void acc_job(const AccJob& j, int64_t t, int slices, 
         if (s0 + u < slices) r[u] = *reinterpret_cast<const Raw*>(src + (int64_t)(s0 + u) * j.n + i0);
 #pragma unroll
       for (int u = 0; u < kAccSlices; ++u) {
-        if (s0 + u >= slices) break;
+        if (s0 + u >= slices) continue;
 #pragma unroll
         for (int e = 0; e < kAccV; ++e) {
           if constexpr (sizeof(T) == 2) v[e] += Elem<T>::from_bits((r[u][e >> 1] >> (16 * (e & 1))) & 0xffffu);
@@ -338,12 +390,10 @@ __device__ __forceinline__ void acc_job(const AccJob& j, int64_t t, int slices, 
     *reinterpret_cast<f32x4_t*>(j.acc + i0) = a;
     return;
   }
-#pragma unroll
   for (int e = 0; e < kAccV; ++e) {
     const int64_t i = i0 + e;
     if (i >= j.n) break;
     float x = first ? 0.f : j.acc[i];
-#pragma unroll 8
     for (int q = 0; q < slices; ++q) x += Elem<T>::load1(src + (int64_t)q * j.n + i);
     j.acc[i] = x;
   }
@@ -384,9 +434,16 @@ static hipError_t launch_im2col(const void* X, void* col, const ConvGeom& g, int
     const int vec = (HWo * (int64_t)sizeof(T)) % 16 == 0 && ((int64_t)TH * g.Wo * sizeof(T)) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(col) % 16 == 0;
     const int xvec = ((int64_t)g.W * sizeof(T)) % 16 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0;
-    hipLaunchKernelGGL((im2col_lds_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       static_cast<unsigned>(band_bytes(TH)), s, static_cast<const T*>(X), static_cast<T*>(col), g,
-                       TH, bands, vec, xvec);
+    // chunked LDS reads: unit horizontal stride, whole runs per output row,
+    // 16-byte LDS rows
+    if (g.sw == 1 && g.Wo % kRun == 0 && xvec)
+      hipLaunchKernelGGL((im2col_lds_kernel<T, true>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                         static_cast<unsigned>(band_bytes(TH)), s, static_cast<const T*>(X), static_cast<T*>(col), g,
+                         TH, bands, vec, xvec);
+    else
+      hipLaunchKernelGGL((im2col_lds_kernel<T, false>), dim3(static_cast<unsigned>(blocks)), dim3(256),
+                         static_cast<unsigned>(band_bytes(TH)), s, static_cast<const T*>(X), static_cast<T*>(col), g,
+                         TH, bands, vec, xvec);
     return hipGetLastError();
   }
   const int runs = static_cast<int>((HWo + kRun - 1) / kRun);

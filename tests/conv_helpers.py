@@ -15,7 +15,12 @@ GEOMS = {
     # kernel the size of the input: a 1x1 output, so the reference-sized gy_rows workspace
     # (Cout*Ho*Wo floats) holds only the dB sum
     "1x1-output": dict(N=3, Cin=4, H=3, W=5, Cout=6, Kh=3, Kw=5, stride=(1, 1), pad=(0, 0), dil=(1, 1)),
+    # unit horizontal stride with 16-byte input rows and Wo a multiple of 8: im2col and col2im
+    # read each run as shifted 16-byte windows (even shifts here, both parities below)
+    "window-dilated": dict(N=2, Cin=3, H=9, W=24, Cout=8, Kh=3, Kw=3, stride=(2, 1), pad=(2, 2), dil=(2, 2)),
+    "window-odd-pad": dict(N=2, Cin=3, H=6, W=16, Cout=5, Kh=3, Kw=5, stride=(1, 1), pad=(1, 2), dil=(1, 1)),
 }
+WINDOW_GEOMS = ("window-dilated", "window-odd-pad")
 
 
 def _attrs(conv, g, act, with_bias, save_z):

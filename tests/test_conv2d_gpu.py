@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import gemm_oracle as O
-from conv_helpers import GEOMS, _inputs, _run
+from conv_helpers import GEOMS, WINDOW_GEOMS, _inputs, _run
 from gemm_helpers import BF16, F32, rounded
 
 pytestmark = pytest.mark.gpu
@@ -62,6 +62,26 @@ def test_conv2d_exact_integers(env, geom, bwd_images):
         d = np.abs(out[k] - ref[k])
         assert np.array_equal(out[k], ref[k]), (k, int((d > 0).sum()), float(d.max()),
                                                 np.unravel_index(int(np.argmax(d)), d.shape))
+
+
+@pytest.mark.parametrize("geom", WINDOW_GEOMS)
+def test_conv2d_exact_integers_bf16(env, geom):
+    """bf16 with entries in {-1, 0, 1}: every sum (at most 120 terms) is an integer that bf16
+    holds exactly, so the shifted-window reads of im2col and col2im are checked bit-exact for
+    16-bit elements at odd and even element offsets."""
+    g = GEOMS[geom]
+    r = np.random.default_rng(11)
+    X = r.integers(-1, 2, (g["N"], g["Cin"], g["H"], g["W"])).astype(np.float32)
+    W = r.integers(-1, 2, (g["Cout"], g["Cin"], g["Kh"], g["Kw"])).astype(np.float32)
+    b = r.integers(-4, 5, g["Cout"]).astype(np.float32)
+    Ho, Wo = O.conv2d_out_size(g["H"], g["W"], g["Kh"], g["Kw"], g["stride"], g["pad"], g["dil"])
+    dY = r.integers(-1, 2, (g["N"], g["Cout"], Ho, Wo)).astype(np.float32)
+    out = _run(env, g, X, W, b, "none", dtype=BF16, all_images=True, dY=dY, bwd_images=2)
+    Y64, Z64 = O.conv2d_forward(X, W, b, g["stride"], g["pad"], g["dil"])
+    assert np.array_equal(out["Z"], Z64) and np.array_equal(out["Y"], Y64)
+    ref = O.conv2d_backward(X, W, dY, Z64, g["stride"], g["pad"], g["dil"])
+    for k in ("dX", "dW", "dB"):
+        assert np.array_equal(out[k], ref[k]), k
 
 
 @pytest.mark.parametrize("act", ["relu", "tanh", "leakyrelu"])
