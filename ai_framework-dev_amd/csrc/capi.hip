@@ -518,6 +518,9 @@ enum PartHome { kPartNone = 0, kPartWorkspace = 1, kPartDx = 2, kPartDw = 3 };
 
 struct BwdScratch {
   bool materialise{false}, prep_vec{false}, sums{false};
+  // the dW (TN) pass finishes dBias from the partials itself (direct-to-LDS
+  // kernel, partials not parked in its own output); it then runs before dX
+  bool sums_in_dw{false};
   int row_blocks{0};
   int part_home{kPartNone};
   int64_t gz_bytes{0};     // dY': batch*M*N elements
@@ -584,6 +587,13 @@ BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
     r.part_home = kPartWorkspace;
     r.need = round256(r.gz_bytes) + r.part_bytes;
   }
+  if (d->gB && r.part_home != kPartDw) {
+    // the dW pass reads dY' (dense, 16-byte rows) as its B operand
+    gev2::TileArgs t{};
+    t.store_vec = out_level(d->gB, dense_ld(d->ldgb, N), d->stride_gb, K, N, batch, dt);
+    const bool vec = vec_ok(d->A, dense_ld(d->lda, K), d->stride_a, K, M, batch, dt);
+    r.sums_in_dw = gev2::dl_selected(dt, pick_cfg(dt, K, N, batch, false), 0, vec, t);
+  }
   return r;
 }
 
@@ -640,6 +650,8 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   // ReLU / LeakyReLU, and the transcendental activations are refused.
   void* ws = nullptr;
   bool sums = sc.sums;
+  const float* dw_part = nullptr;     // dBias partials the dW pass finishes
+  int64_t dw_part_stride = 0;
   if (sc.materialise) {
     if (aligned256(d->workspace) && d->workspace_bytes >= sc.gz_bytes) {
       ws = d->workspace;
@@ -683,7 +695,10 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       }
       e = gev2::launch_grad_prep(dt, pa, batch, s);
       if (e != hipSuccess) return hip_fail(e, "gZ launch");
-      if (sums) {
+      if (sums && sc.sums_in_dw) {
+        dw_part = partial;
+        dw_part_stride = pa.sPartial;
+      } else if (sums) {
         e = gev2::launch_finish_col_sums(partial, pa.sPartial, row_blocks, static_cast<int>(N), d->gBias,
                                          d->stride_gbias, batch, s);
         if (e != hipSuccess) return hip_fail(e, "dBias launch");
@@ -723,7 +738,8 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     }
   }
   // gA[M,K] = alpha * dY' [M,N] * B^T : NT (prologue on A when fused)
-  if (d->gA) {
+  auto run_dx = [&]() -> int {
+    if (!d->gA) return GEV2_OK;
     const bool vec = gyz_vec && vec_ok(d->B, ldb, d->stride_b, N, K, batch, dt);
     if (M <= gev2::kSkinnyMaxM && batch == 1 && vec && env_int("GEV2_NO_SKINNY", 0) == 0) {
       // one wave per output column, each reading one row of B
@@ -786,9 +802,13 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       hipError_t e = gev2::launch_tile(dt, cfg, false, true, fused ? 1 : 0, vec, a, batch, s);
       if (e != hipSuccess) return hip_fail(e, "dX launch");
     }
-  }
-  // gB[K,N] = alpha * A^T [K,M] * dY' [M,N] : TN (prologue on B + fused dBias when fused)
-  if (d->gB) {
+    return GEV2_OK;
+  };
+  // gB[K,N] = alpha * A^T [K,M] * dY' [M,N] : TN (prologue on B + fused dBias
+  // when fused; on a materialised dY' the direct-to-LDS kernel can finish
+  // dBias from grad_prep's partials)
+  auto run_dw = [&]() -> int {
+    if (!d->gB) return GEV2_OK;
     const bool vec = gyz_vec && vec_ok(d->A, lda, d->stride_a, K, M, batch, dt);
     const int cfg = pick_cfg(dt, K, N, batch, fused);
     gev2::TileArgs a{};
@@ -804,9 +824,26 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
     a.tiles_m = static_cast<int>((K + bm - 1) / bm);
     a.tiles_n = static_cast<int>((N + bn - 1) / bn);
     a.store_vec = out_level(d->gB, ldgb, d->stride_gb, K, N, batch, dt);
+    if (dw_part) {
+      if (gev2::dl_selected(dt, cfg, 0, vec, a)) {
+        a.dbias = d->gBias; a.sDbias = d->stride_gbias;
+        a.dbias_part = dw_part; a.sDbiasPart = dw_part_stride; a.dbias_rb = sc.row_blocks;
+      } else {
+        hipError_t e = gev2::launch_finish_col_sums(dw_part, dw_part_stride, sc.row_blocks, static_cast<int>(N),
+                                                    d->gBias, d->stride_gbias, batch, s);
+        if (e != hipSuccess) return hip_fail(e, "dBias launch");
+      }
+      bias_done = true;
+    }
     hipError_t e = gev2::launch_tile(dt, cfg, true, false, fused ? 2 : 0, vec, a, batch, s);
     if (e != hipSuccess) return hip_fail(e, "dW launch");
-  }
+    return GEV2_OK;
+  };
+  // dW first when it reads dBias partials parked in the dX output
+  st = dw_part ? run_dw() : run_dx();
+  if (st != GEV2_OK) return st;
+  st = dw_part ? run_dx() : run_dw();
+  if (st != GEV2_OK) return st;
   if (d->gC || (want_bias && !fuse_bias && !bias_done)) {
     gev2::GradArgs g{};
     g.gY = d->gY; g.Z = d->Z; g.out = d->gC; g.gbias = d->gBias;

@@ -131,16 +131,27 @@ __global__ void __launch_bounds__(256) grad_prep_kernel(PrepArgs p) {
   float sum[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) sum[e] = 0.f;
+  // every load of the thread's rows is issued before the first store (the
+  // output may not be assumed disjoint from the inputs, so stores would
+  // otherwise hold back the next row's loads)
+  constexpr int RPT = kPrepRows / 8;
+  u32x4 g[RPT], z[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int m = r0 + rl + 8 * i;
+    if (nok && m < p.M) {
+      g[i] = *reinterpret_cast<const u32x4*>(gY + (int64_t)m * p.ldgy + n);
+      z[i] = *reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n);
+    }
+  }
   dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = rl; r < kPrepRows; r += 8) {
-      const int m = r0 + r;
+    for (int i = 0; i < RPT; ++i) {
+      const int m = r0 + rl + 8 * i;
       if (!nok || m >= p.M) continue;
-      const u32x4 g = *reinterpret_cast<const u32x4*>(gY + (int64_t)m * p.ldgy + n);
-      const u32x4 z = *reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n);
       float gv[EPC], zv[EPC];
-      chunk_to_f32<T>(g, gv);
-      chunk_to_f32<T>(z, zv);
+      chunk_to_f32<T>(g[i], gv);
+      chunk_to_f32<T>(z[i], zv);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
         gv[e] *= act_grad_t<ACT>(zv[e], p.slope);
@@ -254,7 +265,7 @@ __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
     chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(brow + n0), bv);
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
-      if (m >= p.M) break;
+      if (m >= p.M) continue;
       float gv[EPC];
       chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0), gv);
       if (Z) {
@@ -270,7 +281,7 @@ __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
   T* D = reinterpret_cast<T*>(p.D);
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
-    if (m >= p.M) break;
+    if (m >= p.M) continue;
     float v = acc[m];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);

@@ -190,7 +190,13 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FM][FN], co
 //   q = NQ-1: MFMAs of the last step | step-0 reads of tile t+1 | loads of
 //   tile t+S into stage t % S
 // so a tile's loads are issued S-1 tiles before it is read.
-template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S, int WPE>
+//
+// SUMS (TN layout): after its tile, each workgroup of the first tile row also
+// finishes the PerN bias gradient of its BN columns from the fp32 row-block
+// column sums of B (dbias_part, written by the pass that formed B = dY'):
+// thread groups add disjoint runs of row blocks in order, then the runs are
+// added in order, so no separate launch is needed for the final sum.
+template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S, int WPE, bool SUMS>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_dl_kernel(TileArgs p) {
   static_assert(sizeof(T) == 2, "16-bit element types only");
@@ -317,6 +323,38 @@ gemm_dl_kernel(TileArgs p) {
       store_tile_vec<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds);
     });
   }
+  if constexpr (SUMS) {
+    if (tm == 0) {                                   // uniform over the workgroup
+      constexpr int G = NT / BN;                     // thread groups per column
+      static_assert(G >= 1 && NT % BN == 0, "column groups");
+      const int c = tid % BN, g = tid / BN;
+      const int per = (p.dbias_rb + G - 1) / G;
+      const int rb0 = g * per, rb1 = min(p.dbias_rb, rb0 + per);
+      const int n = n0 + c;
+      float sum = 0.f;
+      if (n < p.N) {
+        const float* pp = p.dbias_part + (int64_t)bz * p.sDbiasPart + n;
+        for (int r = rb0; r < rb1; r += 16) {
+          float v[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) v[u] = r + u < rb1 ? pp[(int64_t)(r + u) * p.N] : 0.f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (r + u < rb1) sum += v[u];
+        }
+      }
+      float* red = reinterpret_cast<float*>(lds);
+      __syncthreads();                               // the epilogue's LDS staging is done
+      red[g * BN + c] = sum;
+      __syncthreads();
+      if (g == 0 && n < p.N) {
+        float s = red[c];
+#pragma unroll
+        for (int q = 1; q < G; ++q) s += red[q * BN + c];
+        p.dbias[(int64_t)bz * p.sDbias + n] = s;
+      }
+    }
+  }
 }
 
 // Waves, K depth and stage count per tile shape.
@@ -335,21 +373,27 @@ template <> struct DlPipe<kCfg256x256> { static constexpr int BK = 64, S = 2, WM
 template <> struct DlPipe<kCfg128x256> { static constexpr int BK = 32, S = 6, WM = 2, WN = 2, WPE = 1; };
 template <> struct DlPipe<kCfg128x128> { static constexpr int BK = 32, S = 4, WM = 2, WN = 2, WPE = 1; };
 
-template <typename T, int CFG, bool TA, bool TB>
+template <typename T, int CFG, bool TA, bool TB, bool SUMS = false>
 static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
   using C = CfgShape<CFG>;
   using P = DlPipe<CFG>;
   dim3 grid(a.tiles_m * a.tiles_n, batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, P::WM, P::WN, TA, TB, P::BK, P::S, P::WPE>), grid,
+  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, P::WM, P::WN, TA, TB, P::BK, P::S, P::WPE, SUMS>), grid,
                      dim3(P::WM * P::WN * 64), 0, s, a);
   return hipGetLastError();
 }
 
+// a.dbias_part set: the TN launch also finishes the PerN dBias (SUMS).
 template <typename T, int CFG>
 static hipError_t launch_dl_layout(bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
+  const bool sums = a.dbias_part != nullptr;
+  if (sums && (!(ta && !tb) || !a.dbias || a.dbias_rb < 1)) return hipErrorInvalidValue;
   if (!ta && !tb) return launch_dl_one<T, CFG, false, false>(a, batch, s);
   if (!ta && tb) return launch_dl_one<T, CFG, false, true>(a, batch, s);
-  if (ta && !tb) return launch_dl_one<T, CFG, true, false>(a, batch, s);
+  if (ta && !tb) {
+    if (sums) return launch_dl_one<T, CFG, true, false, true>(a, batch, s);
+    return launch_dl_one<T, CFG, true, false>(a, batch, s);
+  }
   return hipErrorInvalidValue;
 }
 

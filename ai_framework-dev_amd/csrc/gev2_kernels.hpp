@@ -21,7 +21,11 @@ struct TileArgs {
   const void* A; const void* B; void* D; void* Zo;
   const void* Zi;        // prologue pre-activation (same layout as the operand it scales)
   const float* bias;     // epilogue bias (kind below)
-  float* dbias;          // fused column sums of the prologue operand (PerN dBias)
+  float* dbias;          // PerN dBias: column sums of the prologue operand (PRO == 2), or the
+                         // sum of dbias_part's row blocks (direct-to-LDS TN launch)
+  const float* dbias_part;   // [batch][dbias_rb][N] fp32 row-block column sums of B (or null)
+  int64_t sDbiasPart;
+  int dbias_rb;
   int64_t lda, ldb, ldd, ldzo, ldzi;
   int64_t sA, sB, sD, sZo, sZi, sBias, sDbias;   // batch strides
   int M, N, K;
