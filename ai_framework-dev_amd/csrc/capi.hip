@@ -18,19 +18,26 @@
 
 namespace gev2 {
 
-// The direct-to-LDS kernel (gemm_dl_impl.hpp) takes 16-bit, prologue-free
-// launches with vector loads and stores on the three large tiles; GEV2_DL=0
-// selects the register-staged kernel instead (comparison runs).
+// The direct-to-LDS kernel (gemm_dl_impl.hpp) takes prologue-free launches
+// with vector loads and stores: 16-bit data on the three large tiles, fp32 on
+// those and 64x64.  GEV2_DL=0 selects the register-staged kernel instead
+// (comparison runs).
 bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a) {
-  if (dtype == GEV2_F32 || !vec || pro != 0 || !a.store_vec || cfg == kCfg64x64) return false;
+  if (!vec || pro != 0 || !a.store_vec) return false;
+  if (cfg == kCfg64x64 && dtype != GEV2_F32) return false;
   const char* v = std::getenv("GEV2_DL");
   return !(v && v[0] == '0');
 }
 
 hipError_t launch_tile(int dtype, int cfg, bool ta, bool tb, int pro, bool vec, const TileArgs& a,
                        int batch, hipStream_t s) {
-  if (dl_selected(dtype, cfg, pro, vec, a))
-    return dtype == GEV2_BF16 ? launch_dl_bf16(cfg, ta, tb, a, batch, s) : launch_dl_f16(cfg, ta, tb, a, batch, s);
+  if (dl_selected(dtype, cfg, pro, vec, a)) {
+    switch (dtype) {
+      case GEV2_BF16: return launch_dl_bf16(cfg, ta, tb, a, batch, s);
+      case GEV2_F16: return launch_dl_f16(cfg, ta, tb, a, batch, s);
+      default: return launch_dl_f32(cfg, ta, tb, a, batch, s);
+    }
+  }
   switch (dtype) {
     case GEV2_F32: return launch_tile_f32(cfg, ta, tb, pro, vec, a, batch, s);
     case GEV2_BF16: return launch_tile_bf16(cfg, ta, tb, pro, vec, a, batch, s);
@@ -147,6 +154,7 @@ const char* cfg_name(int cfg, bool vec, bool dl = false) {
       case gev2::kCfg256x256: return "dl:256x256";
       case gev2::kCfg128x128: return "dl:128x128";
       case gev2::kCfg128x256: return "dl:128x256";
+      case gev2::kCfg64x64: return "dl:64x64";
       default: return "dl:?";
     }
   }

@@ -1,5 +1,5 @@
 // Instantiations of the direct-to-LDS MFMA tile GEMM for one element type
-// (__bf16); split per type so the two compile in parallel.
+// (__bf16); split per type so the three compile in parallel.
 #include "gemm_dl_impl.hpp"
 
 namespace gev2 {

@@ -1,0 +1,9 @@
+// Instantiations of the direct-to-LDS MFMA tile GEMM for one element type
+// (float); split per type so the three compile in parallel.
+#include "gemm_dl_impl.hpp"
+
+namespace gev2 {
+hipError_t launch_dl_f32(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
+  return launch_dl_cfg<float>(cfg, ta, tb, a, batch, s);
+}
+}  // namespace gev2

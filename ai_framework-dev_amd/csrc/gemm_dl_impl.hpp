@@ -28,27 +28,35 @@
 
 namespace gev2 {
 
-// Chunk swizzle of K rows.  BK = 64: 8 chunks per 128-byte row, the tile
-// kernel's swz().  BK = 32: 4 chunks per 64-byte row; ((row >> 1) ^ (row >> 3))
-// & 3 gives the rows of equal parity in any aligned 8 (and the rows of equal
+// Chunk swizzle of K rows by row length: 128-byte rows (8 chunks) use the
+// tile kernel's swz(); 64-byte rows (4 chunks) use ((row >> 1) ^ (row >> 3)) & 3,
+// which gives the rows of equal parity in any aligned 8 (and the rows of equal
 // row & 3 in any aligned 16) distinct chunk positions, so fragment reads are
 // conflict free whether a bank cycle serves 128 or 256 bytes.
-template <int BK>
+template <int RBK>
 __device__ __forceinline__ int swz_k(int row) {
-  if constexpr (BK == 64) return swz(row);
+  static_assert(RBK == 64 || RBK == 128, "K row bytes");
+  if constexpr (RBK == 128) return swz(row);
   else return ((row >> 1) ^ (row >> 3)) & 3;
 }
 
-// One operand tile of ROWS (M or N extent) x BK (32 or 64) 16-bit elements.
-template <int ROWS, bool MNC, int NT, int BK>
+// One operand tile of ROWS (M or N extent) x BKB bytes of K, elements of ES
+// bytes (2: bf16 / f16, 4: fp32).  A fragment is one u32x4 per lane: the
+// 16-bit MFMA's 8 k values, or four fp32 k values (one per 32x32x2 MFMA), of
+// row r0 + lane % 32 at k = KF * q + (KF / 2) * (lane / 32) + 0.. within the
+// tile, KF = 32 / ES k per fragment step q.
+template <int ROWS, bool MNC, int NT, int BKB, int ES>
 struct DlStage {
-  static_assert(BK == 32 || BK == 64, "BK");
-  static constexpr int BYTES = ROWS * BK * 2;
+  static_assert(BKB == 64 || BKB == 128, "K tile bytes");
+  static_assert(ES == 2 || ES == 4, "element size");
+  static constexpr int BK = BKB / ES;                         // k per tile
+  static constexpr int EPC = 16 / ES;                         // elements per 16-byte chunk
+  static constexpr int BYTES = ROWS * BKB;
   static constexpr int LOADS = BYTES / 1024;                  // wave instructions per tile
   static constexpr int LPW = LOADS / (NT / 64);               // per wave
-  static constexpr int RB = MNC ? ROWS * 2 : BK * 2;          // LDS row bytes
+  static constexpr int RB = MNC ? ROWS * ES : BKB;            // LDS row bytes
   static_assert(LOADS % (NT / 64) == 0, "tile loads must divide among the waves");
-  static_assert(!MNC || RB >= 128, "MN rows need at least 4 32-byte blocks");
+  static_assert(!MNC || ES == 4 || RB >= 128, "16-bit MN rows need at least 4 32-byte blocks");
 
   int voff[LPW];    // per-lane byte offset of each load at k0 = 0 (kOobOffset if outside)
   int kpos[LPW];    // k of the lane's chunk within the tile
@@ -61,24 +69,29 @@ struct DlStage {
       const int row = byte / RB, off = byte % RB;
       if constexpr (!MNC) {
         // row = M/N index within the tile; logical chunk = physical ^ swizzle
-        const int c = (off / 16) ^ swz_k<BK>(row);
+        const int c = (off / 16) ^ swz_k<BKB>(row);
         const int mn = mn0 + row;
-        kpos[i] = c * 8;
-        voff[i] = mn < MNlim ? static_cast<int>(((int64_t)mn * ld + c * 8) * 2) : kOobOffset;
-      } else {
+        kpos[i] = c * EPC;
+        voff[i] = mn < MNlim ? static_cast<int>(((int64_t)mn * ld + c * EPC) * ES) : kOobOffset;
+      } else if constexpr (ES == 2) {
         // row = k within the tile; logical 32-byte block = physical ^ (k & 3)
         const int lb = (off / 32) ^ (row & 3);
         const int n = lb * 16 + ((off / 16) & 1) * 8;
         const int mn = mn0 + n;
         kpos[i] = row;
         voff[i] = mn < MNlim ? static_cast<int>(((int64_t)row * ld + mn) * 2) : kOobOffset;
+      } else {
+        // fp32: row = k within the tile, stored as it lies in memory
+        const int mn = mn0 + off / 4;
+        kpos[i] = row;
+        voff[i] = mn < MNlim ? static_cast<int>(((int64_t)row * ld + mn) * 4) : kOobOffset;
       }
     }
   }
 
   // Byte offset of K tile k0 from the tile's k = 0 (uniform).
   __device__ __forceinline__ static int kbytes(int k0, int64_t ld) {
-    return MNC ? static_cast<int>(k0 * ld * 2) : k0 * 2;
+    return MNC ? static_cast<int>(k0 * ld * ES) : k0 * ES;
   }
 
   // Issue load I of the K tile at k0 into the LDS buffer at `buf` (uniform).
@@ -89,13 +102,13 @@ struct DlStage {
     dma16(rsrc, off, kb, buf + (wave * LPW + I) * 1024);
   }
 
-  // MFMA fragment (8 elements of k16 step q) for rows/cols [r0, r0 + 32).
+  // MFMA fragment of step q for rows/cols [r0, r0 + 32).
   __device__ __forceinline__ u32x4 frag(const char* buf, int r0, int q, int lane) const {
     if constexpr (!MNC) {
       const int row = r0 + (lane & 31);
       const int ch = 2 * q + (lane >> 5);
-      return *reinterpret_cast<const u32x4*>(buf + row * RB + ((ch ^ swz_k<BK>(row)) * 16));
-    } else {
+      return *reinterpret_cast<const u32x4*>(buf + row * RB + ((ch ^ swz_k<BKB>(row)) * 16));
+    } else if constexpr (ES == 2) {
       const int g = lane >> 4, e = (lane >> 2) & 3, qq = lane & 3;
       const int n = r0 + 16 * (g & 1) + 4 * qq;
       u32x4 out;
@@ -109,6 +122,14 @@ struct DlStage {
         out[2 * h] = w[0];
         out[2 * h + 1] = w[1];
       }
+      return out;
+    } else {
+      // fp32: four k rows, 32 consecutive columns per half-wave
+      const int n = r0 + (lane & 31);
+      const int kb = 8 * q + 4 * (lane >> 5);
+      u32x4 out;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[j] = *reinterpret_cast<const uint32_t*>(buf + (kb + j) * RB + n * 4);
       return out;
     }
   }
@@ -196,18 +217,19 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[FM][FN], co
 // column sums of B (dbias_part, written by the pass that formed B = dY'):
 // thread groups add disjoint runs of row blocks in order, then the runs are
 // added in order, so no separate launch is needed for the final sum.
-template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BK, int S, int WPE, bool SUMS>
+template <typename T, int BM, int BN, int WM, int WN, bool TA, bool TB, int BKB, int S, int WPE, bool SUMS>
 __global__ void __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_dl_kernel(TileArgs p) {
-  static_assert(sizeof(T) == 2, "16-bit element types only");
+  constexpr int ES = sizeof(T);
   constexpr int NT = WM * WN * 64;
-  constexpr int NQ = BK / 16;
+  constexpr int BK = BKB / ES;                 // k per tile
+  constexpr int NQ = BKB / 32;                 // fragment steps per tile
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
   constexpr int NMF = FM * FN, NFR = FM + FN;
   constexpr int H = (NMF + 1) / 2;
-  using SA = DlStage<BM, TA, NT, BK>;
-  using SB = DlStage<BN, !TB, NT, BK>;
+  using SA = DlStage<BM, TA, NT, BKB, ES>;
+  using SB = DlStage<BN, !TB, NT, BKB, ES>;
   constexpr int ABYTES = SA::BYTES, BBYTES = SB::BYTES;
   constexpr int NL = SA::LPW + SB::LPW;   // load instructions per wave per tile
   static_assert(S >= 2 && (S - 1) * NL <= 63, "vmcnt range");
@@ -303,8 +325,9 @@ gemm_dl_kernel(TileArgs p) {
   }
   __builtin_amdgcn_s_waitcnt(0x3f70);   // the loads past the last tile (all out of range)
 
-  // epilogue (the host selects this kernel only with store_vec: 2 = 16-bit
-  // rows with 16-byte aligned starts and N % 8 == 0, staged through LDS)
+  // epilogue (the host selects this kernel only with store_vec != 0; 2 =
+  // 16-bit rows with 16-byte aligned starts and N % 8 == 0, staged through
+  // LDS; 1 = 4-column vector stores from the accumulators)
   float* bias_lds = reinterpret_cast<float*>(lds);
   __syncthreads();
   if (p.bias && p.bias_kind == kBiasPerN) {
@@ -312,13 +335,18 @@ gemm_dl_kernel(TileArgs p) {
     for (int c = tid; c < BN; c += NT) bias_lds[c] = n0 + c < p.N ? biasb[n0 + c] : 0.f;
   }
   __syncthreads();
-  if (p.store_vec == 2) {
-    static_assert(1024 + NT / 64 * 64 * WTN * 2 <= S * (ABYTES + BBYTES), "epilogue staging");
-    char* stage = lds + 1024 + wave * (64 * WTN * 2);
-    dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
-      store_tile_lds<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds, stage);
-    });
-  } else {
+  bool staged = false;
+  if constexpr (ES == 2) {
+    if (p.store_vec == 2) {
+      static_assert(1024 + NT / 64 * 64 * WTN * 2 <= S * (ABYTES + BBYTES), "epilogue staging");
+      char* stage = lds + 1024 + wave * (64 * WTN * 2);
+      dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
+        store_tile_lds<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds, stage);
+      });
+      staged = true;
+    }
+  }
+  if (!staged) {
     dispatch_act(p.act, [&]<int ACT>() __attribute__((always_inline)) {
       store_tile_vec<T, FM, FN, WTM, WTN, ACT>(acc, p, bz, m0, n0, wm, wn, lane, bias_lds);
     });
@@ -368,17 +396,22 @@ gemm_dl_kernel(TileArgs p) {
 //     127.7 us, 16 waves with 5 stages 143 us.
 //   128x256 / 128x128: 4 waves, the most stages of BK = 32 that fit in LDS
 //     (two 128x128 workgroups share a CU).
+//   64x64 (fp32 only): 4 waves of 32x32, four stages of 32 k; a 1024^2 output
+//     is 256 such tiles, one per CU.
+// The K depth is given in bytes (BKB), so fp32 tiles hold half the k of 16-bit
+// ones in the same LDS.
 template <int CFG> struct DlPipe;
-template <> struct DlPipe<kCfg256x256> { static constexpr int BK = 64, S = 2, WM = 2, WN = 4, WPE = 2; };
-template <> struct DlPipe<kCfg128x256> { static constexpr int BK = 32, S = 6, WM = 2, WN = 2, WPE = 1; };
-template <> struct DlPipe<kCfg128x128> { static constexpr int BK = 32, S = 4, WM = 2, WN = 2, WPE = 1; };
+template <> struct DlPipe<kCfg256x256> { static constexpr int BKB = 128, S = 2, WM = 2, WN = 4, WPE = 2; };
+template <> struct DlPipe<kCfg128x256> { static constexpr int BKB = 64, S = 6, WM = 2, WN = 2, WPE = 1; };
+template <> struct DlPipe<kCfg128x128> { static constexpr int BKB = 64, S = 4, WM = 2, WN = 2, WPE = 1; };
+template <> struct DlPipe<kCfg64x64> { static constexpr int BKB = 128, S = 4, WM = 2, WN = 2, WPE = 1; };
 
 template <typename T, int CFG, bool TA, bool TB, bool SUMS = false>
 static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
   using C = CfgShape<CFG>;
   using P = DlPipe<CFG>;
   dim3 grid(a.tiles_m * a.tiles_n, batch);
-  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, P::WM, P::WN, TA, TB, P::BK, P::S, P::WPE, SUMS>), grid,
+  hipLaunchKernelGGL((gemm_dl_kernel<T, C::BM, C::BN, P::WM, P::WN, TA, TB, P::BKB, P::S, P::WPE, SUMS>), grid,
                      dim3(P::WM * P::WN * 64), 0, s, a);
   return hipGetLastError();
 }
@@ -397,14 +430,18 @@ static hipError_t launch_dl_layout(bool ta, bool tb, const TileArgs& a, int batc
   return hipErrorInvalidValue;
 }
 
-// Used for 16-bit data, prologue-free layouts, 16-byte-aligned operands and
-// vector stores, on the 256x256 / 128x256 / 128x128 tiles.
+// Used for prologue-free layouts with 16-byte-aligned operands and vector
+// stores: 16-bit data on the 256x256 / 128x256 / 128x128 tiles, fp32 on those
+// and 64x64.
 template <typename T>
 static hipError_t launch_dl_cfg(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s) {
   switch (cfg) {
     case kCfg256x256: return launch_dl_layout<T, kCfg256x256>(ta, tb, a, batch, s);
     case kCfg128x256: return launch_dl_layout<T, kCfg128x256>(ta, tb, a, batch, s);
     case kCfg128x128: return launch_dl_layout<T, kCfg128x128>(ta, tb, a, batch, s);
+    case kCfg64x64:
+      if constexpr (sizeof(T) == 4) return launch_dl_layout<T, kCfg64x64>(ta, tb, a, batch, s);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

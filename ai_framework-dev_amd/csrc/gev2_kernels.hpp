@@ -125,6 +125,7 @@ hipError_t launch_tile_f16(int cfg, bool ta, bool tb, int pro, bool vec, const T
                            int batch, hipStream_t s);
 hipError_t launch_dl_bf16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
 hipError_t launch_dl_f16(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
+hipError_t launch_dl_f32(int cfg, bool ta, bool tb, const TileArgs& a, int batch, hipStream_t s);
 bool dl_selected(int dtype, int cfg, int pro, bool vec, const TileArgs& a);
 // part: fp32 partial sums for the split-K 16-bit kernel (skinny_split_workspace_bytes)
 hipError_t launch_skinny(int dtype, const SkinnyArgs& a, float* part, hipStream_t s);

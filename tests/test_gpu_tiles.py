@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from oracle import gemm_oracle as O
-from gemm_helpers import BF16, F16, DT_NAMES, Dev, rounded
+from gemm_helpers import BF16, F16, F32, DT_NAMES, Dev, rounded
 
 pytestmark = pytest.mark.gpu
 
@@ -79,6 +79,26 @@ def test_tile_variants_exact(gpu, monkeypatch, cfg, case, kernel):
     layout, M, N, K, pad = case
     Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, BF16, O.BIAS_PERN, "relu", seed=cfg * 7 + M)
     assert path == f"{'dl' if kernel == 'dl' else 'tile'}:{CFGS[cfg]}", path
+    assert np.array_equal(Z, Zr), f"Z {layout} {M}x{N}x{K} {path}"
+    assert np.array_equal(Y, Yr), f"Y {layout} {M}x{N}x{K} {path}"
+
+
+CFGS_F32 = {**CFGS, 2: "64x64"}
+
+
+@pytest.mark.parametrize("cfg", list(CFGS_F32), ids=lambda c: CFGS_F32[c])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}-pad{c[4]}")
+@pytest.mark.parametrize("kernel", ["dl", "pipe"])
+def test_tile_variants_exact_f32(gpu, monkeypatch, cfg, case, kernel):
+    """fp32 on every tile, through the direct-to-LDS kernel (K-contiguous operands read as
+    16-byte fragments, M/N-contiguous ones as four k rows) and the register-staged one."""
+    capi = gpu
+    monkeypatch.setenv("GEV2_TILE_CFG", str(cfg))
+    monkeypatch.setenv("GEV2_DL", "1" if kernel == "dl" else "0")
+    monkeypatch.setenv("GEV2_NO_SPLITK", "1")        # one launch over all of K
+    layout, M, N, K, pad = case
+    Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, F32, O.BIAS_PERN, "relu", seed=cfg * 11 + M)
+    assert path == f"{'dl' if kernel == 'dl' else 'tile'}:{CFGS_F32[cfg]}", path
     assert np.array_equal(Z, Zr), f"Z {layout} {M}x{N}x{K} {path}"
     assert np.array_equal(Y, Yr), f"Y {layout} {M}x{N}x{K} {path}"
 
