@@ -438,7 +438,68 @@ def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=200):
             "kind": "port",
             "sample": f"fp32 numpy forward+backward (np.matmul via {blas}) of the full {M}x{K} @ "
                       f"{K}x{N} ReLU step, {len(ts)} repetitions ({sum(ts):.1f} s wall on {threads} threads), "
-                      f"median {t * 1e3:.1f} ms per step"}
+                      f"median {t * 1e3:.1f} ms per step",
+            "per_config": cpu_config_baselines()}
+
+
+def _cpu_time(fn, budget_s, max_reps=50):
+    """Median seconds of fn() over repetitions filling about budget_s (at least 3)."""
+    fn()
+    ts = []
+    while len(ts) < max_reps and (len(ts) < 3 or sum(ts) < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_config_baselines(budget_s=3.0):
+    """The other BASELINE configs on the same host cores, fp32 numpy (the reference's CPU
+    path as the oracle restates it): C1 and C2 forward + backward steps, C4's two batched
+    products, and C5a's im2col-lowered forward with im2col timed on its own."""
+    from oracle import gemm_oracle as O
+    out = {}
+    g = np.random.default_rng(8)
+    for key, (M, N, K, act) in (("c1_mlp_f32_64x784x256_relu", (64, 256, 784, "relu")),
+                                ("c2_f32_1024_gelu", (1024, 1024, 1024, "gelu"))):
+        X = normal(g, (M, K), 1 / np.sqrt(K))
+        W = normal(g, (K, N), 1 / np.sqrt(K))
+        b = normal(g, (1, N), 0.02)
+        gY = normal(g, (M, N))
+        t, n = _cpu_time(lambda: O.numpy_fp32_step(X, W, b, gY, act), budget_s)
+        out[key] = {"step_us": t * 1e6, "tflops_step": 6.0 * M * N * K / t / 1e12, "reps": n}
+    # C4: 64 slices of Q K^T (scale 1/8) then P V, [64,512,64]
+    Q, Kt, V = (normal(g, (64, 512, 64)) for _ in range(3))
+    P = normal(g, (64, 512, 512))
+    t_qk, n1 = _cpu_time(lambda: np.matmul(Q, Kt.transpose(0, 2, 1)) * np.float32(0.125), budget_s)
+    t_pv, n2 = _cpu_time(lambda: np.matmul(P, V), budget_s)
+    f = 2.0 * 64 * 512 * 512 * 64
+    out["c4_sdpa_batched_f32"] = {"qk_us": t_qk * 1e6, "pv_us": t_pv * 1e6, "tflops_qk": f / t_qk / 1e12,
+                                  "tflops_pv": f / t_pv / 1e12, "reps": n1 + n2}
+    # C5a: X[32,64,56,56], W[128,64,3,3], stride 1, pad 1: col[n, (c,kh,kw), hw], then W col + b, ReLU
+    N_, C, H, Wd, Co = 32, 64, 56, 56, 128
+    Xc = g.random((N_, C, H, Wd), dtype=np.float32)
+    Wc = normal(g, (Co, C * 9), np.sqrt(2 / 576))
+    bc = normal(g, (1, Co, 1), 0.02)
+    Ho, Wo = O.conv2d_out_size(H, Wd, 3, 3, (1, 1), (1, 1), (1, 1))
+
+    def im2col():
+        Xp = np.pad(Xc, ((0, 0), (0, 0), (1, 1), (1, 1)))
+        col = np.empty((N_, C, 9, Ho * Wo), np.float32)
+        for kh in range(3):
+            for kw in range(3):
+                col[:, :, kh * 3 + kw, :] = O._window(Xp, kh, kw, Ho, Wo, (1, 1), (1, 1)).reshape(N_, C, Ho * Wo)
+        return col.reshape(N_, C * 9, Ho * Wo)
+
+    col = im2col()
+    t_col, n1 = _cpu_time(im2col, budget_s, max_reps=10)
+    t_gemm, n2 = _cpu_time(lambda: np.maximum(np.matmul(Wc, col) + bc, np.float32(0)), budget_s, max_reps=10)
+    f = 2.0 * N_ * Ho * Wo * 576 * Co
+    out["c5a_conv_f32"] = {"im2col_us": t_col * 1e6, "gemm_us": t_gemm * 1e6, "fwd_us": (t_col + t_gemm) * 1e6,
+                           "tflops_gemm": f / t_gemm / 1e12, "tflops_fwd": f / (t_col + t_gemm) / 1e12,
+                           "reps": n1 + n2}
+    return {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+            for k, v in out.items()}
 
 
 def measured_traffic():
