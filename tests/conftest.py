@@ -4,7 +4,9 @@ import sys
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-PKG_ROOT = os.path.join(REPO, "ai_framework-dev_amd")
+# GEV2_PKG_ROOT: another directory holding graph_executor_v2 (the sanitizer
+# build of the binding modules); the in-tree package otherwise
+PKG_ROOT = os.environ.get("GEV2_PKG_ROOT") or os.path.join(REPO, "ai_framework-dev_amd")
 for p in (REPO, PKG_ROOT):
     if p not in sys.path:
         sys.path.insert(0, p)

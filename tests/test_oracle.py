@@ -238,7 +238,8 @@ def test_bf16_rounding_known_answers():
 # C restatement (fp32, reference small-kernel order)
 # ---------------------------------------------------------------------------
 def _load_c_oracle():
-    path = os.path.join(REPO, "oracle", "libgemm_oracle.so")
+    # GEV2_ORACLE_LIB: the sanitizer build of the same source
+    path = os.environ.get("GEV2_ORACLE_LIB") or os.path.join(REPO, "oracle", "libgemm_oracle.so")
     if not os.path.exists(path):
         import subprocess
         subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle")], check=True)
