@@ -38,6 +38,12 @@ hipError_t launch_tile(int dtype, int cfg, bool ta, bool tb, int pro, bool vec, 
       default: return launch_dl_f32(cfg, ta, tb, a, batch, s);
     }
   }
+  if (cfg == kCfg128x64) {
+    // the register-staged kernel has no 128x64 tile: 128x128 over the same rows
+    TileArgs b = a;
+    b.tiles_n = (a.N + tile_bn(kCfg128x128, vec) - 1) / tile_bn(kCfg128x128, vec);
+    return launch_tile(dtype, kCfg128x128, ta, tb, pro, vec, b, batch, s);
+  }
   switch (dtype) {
     case GEV2_F32: return launch_tile_f32(cfg, ta, tb, pro, vec, a, batch, s);
     case GEV2_BF16: return launch_tile_bf16(cfg, ta, tb, pro, vec, a, batch, s);
@@ -131,6 +137,7 @@ int pick_cfg(int dtype, int64_t M, int64_t N, int64_t batch, bool fused = false)
       {gev2::kCfg256x256, 256, 256, 1, 1.0},
       {gev2::kCfg128x256, 128, 256, 1, 0.85},
       {gev2::kCfg128x128, 128, 128, 2, 0.7},
+      {gev2::kCfg128x64, 128, 64, 2, 0.6},
       {gev2::kCfg64x64, 64, 64, 4, 0.35},
   };
   (void)dtype;
@@ -155,6 +162,7 @@ const char* cfg_name(int cfg, bool vec, bool dl = false) {
       case gev2::kCfg128x128: return "dl:128x128";
       case gev2::kCfg128x256: return "dl:128x256";
       case gev2::kCfg64x64: return "dl:64x64";
+      case gev2::kCfg128x64: return "dl:128x64";
       default: return "dl:?";
     }
   }
@@ -163,6 +171,7 @@ const char* cfg_name(int cfg, bool vec, bool dl = false) {
     case gev2::kCfg128x128: return "tile:128x128";
     case gev2::kCfg64x64: return "tile:64x64";
     case gev2::kCfg128x256: return "tile:128x256";
+    case gev2::kCfg128x64: return "tile:128x128";   // launched as 128x128
     default: return "tile:?";
   }
 }

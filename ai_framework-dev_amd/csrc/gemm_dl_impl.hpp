@@ -414,6 +414,9 @@ gemm_dl_kernel(TileArgs p) {
 //     (two 128x128 workgroups share a CU).
 //   64x64 (fp32 only): 4 waves of 32x32, four stages of 32 k; a 1024^2 output
 //     is 256 such tiles, one per CU.
+//   128x64: 4 waves of 32x64, three stages of 128 bytes of K (72 KB for 16-bit,
+//     so two workgroups share a CU): narrow outputs such as attention's P.V
+//     (N = 64), which a 128-wide tile would half waste.
 // The K depth is given in bytes (BKB), so fp32 tiles hold half the k of 16-bit
 // ones in the same LDS.
 template <int CFG> struct DlPipe;
@@ -421,6 +424,7 @@ template <> struct DlPipe<kCfg256x256> { static constexpr int BKB = 128, S = 2, 
 template <> struct DlPipe<kCfg128x256> { static constexpr int BKB = 64, S = 6, WM = 2, WN = 2, WPE = 1; };
 template <> struct DlPipe<kCfg128x128> { static constexpr int BKB = 64, S = 4, WM = 2, WN = 2, WPE = 1; };
 template <> struct DlPipe<kCfg64x64> { static constexpr int BKB = 128, S = 4, WM = 2, WN = 2, WPE = 1; };
+template <> struct DlPipe<kCfg128x64> { static constexpr int BKB = 128, S = 3, WM = 4, WN = 1, WPE = 1; };
 
 template <typename T, int CFG, bool TA, bool TB, bool SUMS = false>
 static hipError_t launch_dl_one(const TileArgs& a, int batch, hipStream_t s) {
@@ -455,6 +459,7 @@ static hipError_t launch_dl_cfg(int cfg, bool ta, bool tb, const TileArgs& a, in
     case kCfg256x256: return launch_dl_layout<T, kCfg256x256>(ta, tb, a, batch, s);
     case kCfg128x256: return launch_dl_layout<T, kCfg128x256>(ta, tb, a, batch, s);
     case kCfg128x128: return launch_dl_layout<T, kCfg128x128>(ta, tb, a, batch, s);
+    case kCfg128x64: return launch_dl_layout<T, kCfg128x64>(ta, tb, a, batch, s);
     case kCfg64x64:
       if constexpr (sizeof(T) == 4) return launch_dl_layout<T, kCfg64x64>(ta, tb, a, batch, s);
       return hipErrorInvalidValue;

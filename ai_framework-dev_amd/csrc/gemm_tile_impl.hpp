@@ -995,6 +995,7 @@ gemm_pipe_kernel(TileArgs p) {
 template <int CFG> struct CfgShape;
 template <> struct CfgShape<kCfg256x256> { static constexpr int BM = 256, BN = 256, WM = 2, WN = 2; };
 template <> struct CfgShape<kCfg128x128> { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2; };
+template <> struct CfgShape<kCfg128x64> { static constexpr int BM = 128, BN = 64, WM = 4, WN = 1; };
 template <> struct CfgShape<kCfg64x64> { static constexpr int BM = 64, BN = 64, WM = 2, WN = 2; };
 template <> struct CfgShape<kCfg128x256> { static constexpr int BM = 128, BN = 256, WM = 2, WN = 2; };
 

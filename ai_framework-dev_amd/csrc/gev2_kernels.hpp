@@ -109,10 +109,11 @@ hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int ro
 // Launcher entry points (each returns hipError_t from the launch).
 // Tile configuration ids, chosen by the host dispatcher.
 enum TileCfg : int {
-  kCfg256x256 = 0,   // 256x256, 4 waves (128x128 per wave)
+  kCfg256x256 = 0,   // 256x256 (direct-to-LDS: 8 waves of 128x64; register-staged: 4 of 128x128)
   kCfg128x128 = 1,   // 128x128, 4 waves (64x64 per wave)
   kCfg64x64 = 2,     // 64x64, 4 waves (32x32 per wave)
   kCfg128x256 = 3,   // 128x256, 4 waves (64x128 per wave)
+  kCfg128x64 = 4,    // 128x64, 4 waves (32x64 per wave; direct-to-LDS kernel only)
 };
 
 hipError_t launch_tile(int dtype, int cfg, bool trans_a, bool trans_b, int prologue,
@@ -153,7 +154,7 @@ inline int tile_bm(int cfg, bool vec) {
 }
 inline int tile_bn(int cfg, bool vec) {
   if (!vec) return 64;
-  return cfg == kCfg256x256 ? 256 : cfg == kCfg64x64 ? 64 : cfg == kCfg128x256 ? 256 : 128;
+  return cfg == kCfg256x256 ? 256 : cfg == kCfg64x64 || cfg == kCfg128x64 ? 64 : cfg == kCfg128x256 ? 256 : 128;
 }
 
 }  // namespace gev2

@@ -1,7 +1,7 @@
 """GPU parity of every large-tile kernel variant, forced one at a time.
 
 The tile dispatcher picks the kernel by cost; here GEV2_TILE_CFG pins the tile
-(256x256, 128x256, 128x128) so that each shape runs through each variant:
+(256x256, 128x256, 128x128, 128x64) so that each shape runs through each variant:
 the direct-to-LDS kernel for 16-bit data (both epilogue forms: LDS-staged
 16-byte rows when N % 8 == 0, 4-column stores when only N % 4 == 0), and
 with GEV2_DL=0 the register-staged kernel it replaces.
@@ -21,7 +21,9 @@ from gemm_helpers import BF16, F16, F32, DT_NAMES, Dev, rounded
 
 pytestmark = pytest.mark.gpu
 
-CFGS = {0: "256x256", 3: "128x256", 1: "128x128"}
+CFGS = {0: "256x256", 3: "128x256", 1: "128x128", 4: "128x64"}
+# the register-staged kernel has no 128x64 tile and runs that request as 128x128
+PIPE_NAME = {**{c: n for c, n in CFGS.items()}, 4: "128x128"}
 
 # (layout, M, N, K, ldy_pad): NT keeps K contiguous on both operands, so N may
 # be 4 mod 8 there (the 4-column epilogue); NN / TN need N (and TN M) % 8 == 0
@@ -78,7 +80,7 @@ def test_tile_variants_exact(gpu, monkeypatch, cfg, case, kernel):
     monkeypatch.setenv("GEV2_DL", "1" if kernel == "dl" else "0")
     layout, M, N, K, pad = case
     Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, BF16, O.BIAS_PERN, "relu", seed=cfg * 7 + M)
-    assert path == f"{'dl' if kernel == 'dl' else 'tile'}:{CFGS[cfg]}", path
+    assert path == (f"dl:{CFGS[cfg]}" if kernel == "dl" else f"tile:{PIPE_NAME[cfg]}"), path
     assert np.array_equal(Z, Zr), f"Z {layout} {M}x{N}x{K} {path}"
     assert np.array_equal(Y, Yr), f"Y {layout} {M}x{N}x{K} {path}"
 
@@ -98,7 +100,7 @@ def test_tile_variants_exact_f32(gpu, monkeypatch, cfg, case, kernel):
     monkeypatch.setenv("GEV2_NO_SPLITK", "1")        # one launch over all of K
     layout, M, N, K, pad = case
     Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, F32, O.BIAS_PERN, "relu", seed=cfg * 11 + M)
-    assert path == f"{'dl' if kernel == 'dl' else 'tile'}:{CFGS_F32[cfg]}", path
+    assert path == (f"dl:{CFGS_F32[cfg]}" if kernel == "dl" else f"tile:{PIPE_NAME.get(cfg, CFGS_F32[cfg])}"), path
     assert np.array_equal(Z, Zr), f"Z {layout} {M}x{N}x{K} {path}"
     assert np.array_equal(Y, Yr), f"Y {layout} {M}x{N}x{K} {path}"
 
