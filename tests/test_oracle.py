@@ -45,6 +45,18 @@ def test_act_special_values():
     assert np.all(d(np.linspace(-5, 5, 11), "none") == 1.0)
 
 
+def test_gelu_constants():
+    """c is fixed by the mathematics (sqrt(2/pi), to the 10 digits activations.hpp:19 writes), and
+    the whole tanh form, k1 = 0.044715 included, agrees with an independent implementation of the
+    same approximation (torch's gelu(approximate='tanh'), float64) to 1e-12: a wrong digit in either
+    constant moves it by more than 1e-6."""
+    import torch
+    assert abs(O.GELU_C - np.sqrt(2 / np.pi)) < 5e-11
+    z = np.linspace(-8, 8, 20001)
+    ref = torch.nn.functional.gelu(torch.from_numpy(z), approximate="tanh").numpy()
+    assert np.max(np.abs(O.act_forward(z, "gelu") - ref)) < 1e-11
+
+
 def test_gelu_tanh_form_tracks_erf_form():
     z = np.linspace(-8, 8, 4001)
     # the tanh approximation of GELU is within 1e-3 of the exact erf form
