@@ -11,7 +11,8 @@
 //     fragments are read with one ds_read_b128 each;
 //   - an operand contiguous along M/N ("MN rows") is stored as it lies in
 //     memory, one row per k, with the 32-byte block index XOR-swizzled by
-//     (k & 3), and its fragments are read with two ds_read_b64_tr_b16, which
+//     2 (k & 3) (k & 3 for 128-byte rows), and its fragments are read with
+//     two ds_read_b64_tr_b16, which
 //     transpose 4x16 blocks of 16-bit elements across each 16-lane group:
 //     lane 16g+i receives element e of the 8-byte chunk addressed by lane
 //     16g+4e+i/4, at position i%4.
@@ -61,6 +62,13 @@ struct DlStage {
   int voff[LPW];    // per-lane byte offset of each load at k0 = 0 (kOobOffset if outside)
   int kpos[LPW];    // k of the lane's chunk within the tile
 
+  // 32-byte block swizzle of 16-bit MN rows.  A half-wave of a transpose read
+  // takes two adjacent blocks (an even-odd pair) from each of four consecutive
+  // rows; XOR with 2 * (k & 3) puts those eight blocks in eight different
+  // 32-byte bank groups when a row has at least 8 blocks (with k & 3 alone,
+  // rows k and k ^ 1 share the pair's two groups).  Rows of 4 blocks keep k & 3.
+  __device__ __forceinline__ static int mn_swz(int k) { return RB >= 256 ? 2 * (k & 3) : (k & 3); }
+
   // mn0: tile origin along M/N; MNlim: extent; ld: leading dimension (elements)
   __device__ __forceinline__ void init(int64_t ld, int mn0, int MNlim, int wave, int lane) {
 #pragma unroll
@@ -74,8 +82,8 @@ struct DlStage {
         kpos[i] = c * EPC;
         voff[i] = mn < MNlim ? static_cast<int>(((int64_t)mn * ld + c * EPC) * ES) : kOobOffset;
       } else if constexpr (ES == 2) {
-        // row = k within the tile; logical 32-byte block = physical ^ (k & 3)
-        const int lb = (off / 32) ^ (row & 3);
+        // row = k within the tile; logical 32-byte block = physical ^ mn_swz(k)
+        const int lb = (off / 32) ^ mn_swz(row);
         const int n = lb * 16 + ((off / 16) & 1) * 8;
         const int mn = mn0 + n;
         kpos[i] = row;
@@ -115,7 +123,7 @@ struct DlStage {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int k = 16 * q + 8 * (g >> 1) + 4 * h + e;
-        const char* p = buf + k * RB + (((n >> 4) ^ (k & 3)) << 5) + (n & 15) * 2;
+        const char* p = buf + k * RB + (((n >> 4) ^ mn_swz(k)) << 5) + (n & 15) * 2;
         const s16x4_t v =
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)(p));
         const u32x2 w = __builtin_bit_cast(u32x2, v);
