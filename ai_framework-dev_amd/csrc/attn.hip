@@ -111,9 +111,32 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(const u32x4& a, const u32x4& b,
 
 __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
-// LDS image of one key block: K rows with 16-byte chunks XOR-swizzled by
-// (row & 7) (rows read whole for the A operand), V rows with 32-byte blocks
-// XOR-swizzled by (row & 3) (read with transpose reads).
+// Every 64- or 128-element 16-bit row tile in LDS here (K, V, Q, dO) stores
+// row r's logical 16-byte chunk c at physical chunk c ^ att_swz<D>(r).  Two
+// read patterns use the tiles: 16-byte row reads in which 8 consecutive lanes
+// take one chunk of 8 consecutive rows (MFMA operands read whole), and
+// transpose reads in which a half-wave takes one 32-byte block (two chunks) of
+// 8 consecutive, 8-aligned rows.  Measured with the LDS bank-conflict counter
+// on gfx950, the row reads are conflict free when those 8 rows' chunks differ
+// in their low three bits, and the transpose reads when the 8 blocks differ in
+// chunk bits 1-3 (with 128-byte rows, two rows share a bank period and the
+// parity of the row separates them).  row & 7 gives both for D = 64; for
+// D = 128, (row & 7) | ((row & 1) << 3) does (row & 7 alone, row & 15, or a
+// 32-byte block swizzle each leave one pattern two-way conflicted).
+template <int D>
+__device__ __forceinline__ int att_swz(int row) {
+  if constexpr (D == 128) return (row & 7) | ((row & 1) << 3);
+  else return row & 7;
+}
+
+// Address of logical 16-byte chunk `chunk` of `row` in a tile of 2D-byte rows.
+template <int D>
+__device__ __forceinline__ const char* att_chunk(const char* base, int row, int chunk) {
+  return base + row * (2 * D) + ((chunk ^ att_swz<D>(row)) << 4);
+}
+
+// LDS image of one key block: K rows (read whole for the A operand) and V rows
+// (read with transpose reads), both in the att_swz layout.
 template <int D, int KT>
 struct KvBlock {
   static constexpr int kKeys = 16 * KT;
@@ -135,11 +158,10 @@ __device__ __forceinline__ void load_kv(const i32x4_t& rK, const i32x4_t& rV, in
     const int row = ld * rows_per_load + lane / B::kChunks;
     const int pc = lane % B::kChunks;                         // physical 16-byte chunk
     const int key = key0 + row;
-    const int ck = pc ^ (row & 7);                            // K: logical chunk
-    const int cv = (((pc >> 1) ^ (row & 3)) << 1) | (pc & 1); // V: logical chunk
+    const int c = pc ^ att_swz<D>(row);                       // logical chunk
     const bool in = key < N;
-    const int offk = in ? static_cast<int>(((head_off + key) * D + ck * 8) * 2) : kOobOffset;
-    const int offv = in ? static_cast<int>(((head_off + key) * D + cv * 8) * 2) : kOobOffset;
+    const int offk = in ? static_cast<int>(((head_off + key) * D + c * 8) * 2) : kOobOffset;
+    const int offv = in ? static_cast<int>(((head_off + key) * D + c * 8) * 2) : kOobOffset;
     dma16(rK, offk, 0, k_lds + ld * 1024);
     dma16(rV, offv, 0, v_lds + ld * 1024);
   }
@@ -240,8 +262,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
       for (int qt = 0; qt < QT; ++qt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int c = (4 * ks + g) ^ (row & 7);
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(kl + row * B::kRowBytes + c * 16);
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(att_chunk<D>(kl, row, 4 * ks + g));
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) s[qt][kt] = mfma_16x16x32<T>(kf, qf[qt][ks], s[qt][kt]);
       }
@@ -333,8 +354,8 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
         for (int h = 0; h < 2; ++h) {
           const int row = 32 * j + 16 * h + 4 * g + e;
           const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4_t*)(vl + row * B::kRowBytes + ((dt ^ (row & 3)) << 5) +
-                                                           cq * 8));
+              (__attribute__((address_space(3))) s16x4_t*)(att_chunk<D>(vl, row, 2 * dt + (cq >> 1)) +
+                                                           (cq & 1) * 8));
           const u32x2 w2 = __builtin_bit_cast(u32x2, v);
           vf[2 * h] = w2[0];
           vf[2 * h + 1] = w2[1];
@@ -510,23 +531,23 @@ __global__ void __launch_bounds__(256) attn_bwd_dot_kernel(const T* __restrict__
   if (sub == 0) Dq[(row / M) * ld + row % M] = acc;
 }
 
-// 16-byte row piece (8 elements from 8 * chunk) of a tile whose rows hold
-// 32-byte blocks XOR-swizzled by (row & 3)
-__device__ __forceinline__ u32x4 row16_b32swz(const char* base, int row_bytes, int row, int chunk) {
-  return *reinterpret_cast<const u32x4*>(base + row * row_bytes + ((((chunk >> 1) ^ (row & 3))) << 5) +
-                                         ((chunk & 1) << 4));
+// 16-byte row piece (8 elements from 8 * chunk) of an att_swz tile
+template <int D>
+__device__ __forceinline__ u32x4 row16(const char* base, int row, int chunk) {
+  return *reinterpret_cast<const u32x4*>(att_chunk<D>(base, row, chunk));
 }
 
 // Transpose-read operand: lane 16g + i receives rows {r0 + 4g + e, r0 + 16 + 4g + e}
-// (e = 0..3) of column 16 dt + i from a tile with 32-byte blocks swizzled by (row & 3).
-__device__ __forceinline__ u32x4 tr_operand(const char* base, int row_bytes, int r0, int dt, int lane) {
+// (e = 0..3) of column 16 dt + i from an att_swz tile.
+template <int D>
+__device__ __forceinline__ u32x4 tr_operand(const char* base, int r0, int dt, int lane) {
   const int g = lane >> 4, e = (lane >> 2) & 3, cq = lane & 3;
   u32x4 f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = r0 + 16 * h + 4 * g + e;
     const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4_t*)(base + row * row_bytes + ((dt ^ (row & 3)) << 5) + cq * 8));
+        (__attribute__((address_space(3))) s16x4_t*)(att_chunk<D>(base, row, 2 * dt + (cq >> 1)) + (cq & 1) * 8));
     const u32x2 w2 = __builtin_bit_cast(u32x2, v);
     f[2 * h] = w2[0];
     f[2 * h + 1] = w2[1];
@@ -547,9 +568,9 @@ __device__ __forceinline__ bool masked_entry(const AttnArgs& a, int b, int q, in
 }
 
 // DMA one 64-row tile of a [rows, D] tensor (rows past `limit` read as zero)
-// into LDS with 32-byte blocks swizzled by (row & 3); this wave's share.
+// into LDS in the att_swz layout; this wave's share.
 template <int D>
-__device__ __forceinline__ void load_rows_b32swz(const i32x4_t& r, int64_t head_off, int row0, int limit, int wave,
+__device__ __forceinline__ void load_rows(const i32x4_t& r, int64_t head_off, int row0, int limit, int wave,
                                                  int lane, uint32_t lds) {
   constexpr int kRowBytes = D * 2, kChunks = D / 8, rows_per_load = 1024 / kRowBytes;
   constexpr int loads = 64 * kRowBytes / 1024 / 4;
@@ -558,24 +579,7 @@ __device__ __forceinline__ void load_rows_b32swz(const i32x4_t& r, int64_t head_
     const int ld = wave * loads + j;
     const int row = ld * rows_per_load + lane / kChunks;
     const int pc = lane % kChunks;
-    const int c = (((pc >> 1) ^ (row & 3)) << 1) | (pc & 1);
-    const int off = row0 + row < limit ? static_cast<int>(((head_off + row0 + row) * D + c * 8) * 2) : kOobOffset;
-    dma16(r, off, 0, lds + ld * 1024);
-  }
-}
-
-// Same with 16-byte chunks swizzled by (row & 7) (rows read whole only).
-template <int D>
-__device__ __forceinline__ void load_rows_c16swz(const i32x4_t& r, int64_t head_off, int row0, int limit, int wave,
-                                                 int lane, uint32_t lds) {
-  constexpr int kRowBytes = D * 2, kChunks = D / 8, rows_per_load = 1024 / kRowBytes;
-  constexpr int loads = 64 * kRowBytes / 1024 / 4;
-#pragma unroll
-  for (int j = 0; j < loads; ++j) {
-    const int ld = wave * loads + j;
-    const int row = ld * rows_per_load + lane / kChunks;
-    const int pc = lane % kChunks;
-    const int c = pc ^ (row & 7);
+    const int c = pc ^ att_swz<D>(row);
     const int off = row0 + row < limit ? static_cast<int>(((head_off + row0 + row) * D + c * 8) * 2) : kOobOffset;
     dma16(r, off, 0, lds + ld * 1024);
   }
@@ -641,16 +645,16 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
     dma16(rD, off, 0, abase + st * 2048 + 1024);
   };
   if (qb0 < nqb) {
-    load_rows_b32swz<D>(rQ, qhead, qb0 * 64, a.M, wave, lane, q_lds(0));
-    load_rows_b32swz<D>(rO, qhead, qb0 * 64, a.M, wave, lane, o_lds(0));
+    load_rows<D>(rQ, qhead, qb0 * 64, a.M, wave, lane, q_lds(0));
+    load_rows<D>(rO, qhead, qb0 * 64, a.M, wave, lane, o_lds(0));
     if (wave == 0) load_aux(qb0 * 64, 0);
   }
   for (int qb = qb0; qb < nqb; ++qb) {
     const int st = STAGES == 2 ? (qb - qb0) & 1 : 0;
     if constexpr (STAGES == 2) {
       if (qb + 1 < nqb) {
-        load_rows_b32swz<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
-        load_rows_b32swz<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
+        load_rows<D>(rQ, qhead, (qb + 1) * 64, a.M, wave, lane, q_lds(st ^ 1));
+        load_rows<D>(rO, qhead, (qb + 1) * 64, a.M, wave, lane, o_lds(st ^ 1));
         if (wave == 0) {
           load_aux((qb + 1) * 64, st ^ 1);
           __builtin_amdgcn_s_waitcnt(0x3f70 | ((NL + 2) & 0xf) | (((NL + 2) >> 4) << 14));
@@ -663,8 +667,8 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
     } else {
       // the barrier that ended the previous block's use of stage 0 is behind us
       if (qb > qb0) {
-        load_rows_b32swz<D>(rQ, qhead, qb * 64, a.M, wave, lane, q_lds(0));
-        load_rows_b32swz<D>(rO, qhead, qb * 64, a.M, wave, lane, o_lds(0));
+        load_rows<D>(rQ, qhead, qb * 64, a.M, wave, lane, q_lds(0));
+        load_rows<D>(rO, qhead, qb * 64, a.M, wave, lane, o_lds(0));
         if (wave == 0) load_aux(qb * 64, 0);
       }
       __builtin_amdgcn_s_waitcnt(0x3f70);
@@ -681,8 +685,8 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
       f32x4_t sacc = f32x4_t{0.f, 0.f, 0.f, 0.f}, pacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        sacc = mfma_16x16x32<T>(row16_b32swz(ql, RB, 16 * t + col, 4 * ks + g), kf[ks], sacc);
-        pacc = mfma_16x16x32<T>(row16_b32swz(ol, RB, 16 * t + col, 4 * ks + g), vf[ks], pacc);
+        sacc = mfma_16x16x32<T>(row16<D>(ql, 16 * t + col, 4 * ks + g), kf[ks], sacc);
+        pacc = mfma_16x16x32<T>(row16<D>(ol, 16 * t + col, 4 * ks + g), vf[ks], pacc);
       }
       float p[4], ds[4];
 #pragma unroll
@@ -722,8 +726,8 @@ attn_bwd_kv_kernel(AttnBwdArgs ba) {
       const u32x4 sb = {sw[2 * i][0], sw[2 * i][1], sw[2 * i + 1][0], sw[2 * i + 1][1]};
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        dv[dt] = mfma_16x16x32<T>(tr_operand(ol, RB, 32 * i, dt, lane), pb, dv[dt]);
-        dk[dt] = mfma_16x16x32<T>(tr_operand(ql, RB, 32 * i, dt, lane), sb, dk[dt]);
+        dv[dt] = mfma_16x16x32<T>(tr_operand<D>(ol, 32 * i, dt, lane), pb, dv[dt]);
+        dk[dt] = mfma_16x16x32<T>(tr_operand<D>(ql, 32 * i, dt, lane), sb, dk[dt]);
       }
     }
     __syncthreads();
@@ -793,14 +797,14 @@ attn_bwd_q_kernel(AttnBwdArgs ba) {
   const uint32_t base = lds_addr(&lds[0][0][0]);
   auto k_lds = [&](int st) { return base + st * 2 * TILE; };
   auto v_lds = [&](int st) { return base + st * 2 * TILE + TILE; };
-  load_rows_b32swz<D>(rK, khead, 0, a.N, wave, lane, k_lds(0));
-  load_rows_c16swz<D>(rV, khead, 0, a.N, wave, lane, v_lds(0));
+  load_rows<D>(rK, khead, 0, a.N, wave, lane, k_lds(0));
+  load_rows<D>(rV, khead, 0, a.N, wave, lane, v_lds(0));
   for (int kb = 0; kb < nkb; ++kb) {
     const int st = STAGES == 2 ? kb & 1 : 0;
     if constexpr (STAGES == 2) {
       if (kb + 1 < nkb) {
-        load_rows_b32swz<D>(rK, khead, (kb + 1) * 64, a.N, wave, lane, k_lds(st ^ 1));
-        load_rows_c16swz<D>(rV, khead, (kb + 1) * 64, a.N, wave, lane, v_lds(st ^ 1));
+        load_rows<D>(rK, khead, (kb + 1) * 64, a.N, wave, lane, k_lds(st ^ 1));
+        load_rows<D>(rV, khead, (kb + 1) * 64, a.N, wave, lane, v_lds(st ^ 1));
         __builtin_amdgcn_s_waitcnt(0x3f70 | (NL & 0xf) | ((NL >> 4) << 14));
       } else {
         __builtin_amdgcn_s_waitcnt(0x3f70);
@@ -808,8 +812,8 @@ attn_bwd_q_kernel(AttnBwdArgs ba) {
     } else {
       // the barrier that ended the previous block's use of stage 0 is behind us
       if (kb > 0) {
-        load_rows_b32swz<D>(rK, khead, kb * 64, a.N, wave, lane, k_lds(0));
-        load_rows_c16swz<D>(rV, khead, kb * 64, a.N, wave, lane, v_lds(0));
+        load_rows<D>(rK, khead, kb * 64, a.N, wave, lane, k_lds(0));
+        load_rows<D>(rV, khead, kb * 64, a.N, wave, lane, v_lds(0));
       }
       __builtin_amdgcn_s_waitcnt(0x3f70);
     }
@@ -824,9 +828,8 @@ attn_bwd_q_kernel(AttnBwdArgs ba) {
       const int row = 16 * kt + col;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        sacc = mfma_16x16x32<T>(row16_b32swz(kl, RB, row, 4 * ks + g), qf[ks], sacc);
-        const int c = (4 * ks + g) ^ (row & 7);
-        pacc = mfma_16x16x32<T>(*reinterpret_cast<const u32x4*>(vl + row * RB + c * 16), of[ks], pacc);
+        sacc = mfma_16x16x32<T>(row16<D>(kl, row, 4 * ks + g), qf[ks], sacc);
+        pacc = mfma_16x16x32<T>(row16<D>(vl, row, 4 * ks + g), of[ks], pacc);
       }
       float ds[4];
 #pragma unroll
@@ -854,7 +857,7 @@ attn_bwd_q_kernel(AttnBwdArgs ba) {
     for (int j = 0; j < 2; ++j) {
       const u32x4 sb = {sw[2 * j][0], sw[2 * j][1], sw[2 * j + 1][0], sw[2 * j + 1][1]};
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma_16x16x32<T>(tr_operand(kl, RB, 32 * j, dt, lane), sb, acc[dt]);
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma_16x16x32<T>(tr_operand<D>(kl, 32 * j, dt, lane), sb, acc[dt]);
     }
     __syncthreads();
   }
