@@ -31,7 +31,7 @@ INCLUDE = os.path.join(REPO, "include")
 HIP_SOURCES = [
     "gemm_tile_f32.hip", "gemm_tile_bf16.hip", "gemm_tile_f16.hip",
     "gemm_dl_bf16.hip", "gemm_dl_f16.hip", "gemm_dl_f32.hip",
-    "gemm_skinny.hip", "gemm_aux.hip", "capi.hip", "noalloc.hip", "conv.hip", "rnn.hip", "attn.hip", "probe.hip",
+    "gemm_skinny.hip", "gemm_small.hip", "gemm_aux.hip", "capi.hip", "noalloc.hip", "conv.hip", "rnn.hip", "attn.hip", "probe.hip",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -264,7 +264,33 @@ struct FwdPlan {
   // partial products [ksplit][M][N] fp32 in the workspace (ws_bytes)
   int ksplit = 0;
   int64_t kc = 0, kc_last = 0;
+  // small fp32 problem: one launch of the small kernel with this many waves
+  // per workgroup (0: not taken)
+  int small_waves = 0;
 };
+
+// Small fp32 problems run in one launch of the small kernel (16x16 output
+// tiles, the reduction split over the waves of a workgroup): at most 512
+// tiles, a reduction of 128-2048 and 2^26 multiply-adds, where the tile
+// kernels would run as a handful of workgroups (or split K over a second
+// pass).  GEV2_NO_SMALL=1 turns it off.
+int small_waves_for(int64_t red) { return red >= 512 ? 16 : 4; }
+
+// a small-kernel operand, with its 16-byte-load flag
+gev2::SmallOperand small_op(const void* p, int64_t rs, int64_t ks, const void* z = nullptr, int64_t zrs = 0,
+                            int64_t zks = 0) {
+  gev2::SmallOperand o{static_cast<const float*>(p), rs, ks, static_cast<const float*>(z), zrs, zks, 0};
+  o.vec = ks == 1 && rs % 4 == 0 && aligned16(p) && (!z || (zks == 1 && zrs % 4 == 0 && aligned16(z)));
+  return o;
+}
+
+void plan_small(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
+  const int64_t M = d->M, N = d->N, K = d->K;
+  if (d->dtype != GEV2_F32 || d->batch != 1 || env_int("GEV2_NO_SMALL", 0) != 0) return;
+  const int64_t tiles = ((M + 15) / 16) * ((N + 15) / 16);
+  if (tiles > 512 || K < 128 || K > 2048 || static_cast<double>(M) * N * K > 67108864.0) return;
+  pl->small_waves = small_waves_for(K);
+}
 
 // Slices of a split reduction of depth R over `tiles` output tiles: enough
 // slices for about 128 workgroups, each at least 16 deep.  A slice depth (a
@@ -330,7 +356,8 @@ int plan_fwd(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
   pl->skinny = d->batch == 1 && !ta && !tb && M <= gev2::kSkinnyMaxM && K >= 64 && N % epc == 0 &&
                vec_ok(d->B, pl->ldb, 0, N, K, 1, d->dtype) && env_int("GEV2_NO_SKINNY", 0) == 0;
   if (!pl->skinny) {
-    plan_splitk(d, pl);
+    plan_small(d, pl);
+    if (!pl->small_waves) plan_splitk(d, pl);
     return GEV2_OK;
   }
   const bool has_bias = d->bias && d->bias_kind != GEV2_BIAS_NONE;
@@ -435,6 +462,28 @@ int gemm_fwd_run(const gev2_gemm_fwd_desc* d, void* stream, void* fixed, int64_t
     hipError_t e = gev2::launch_skinny(d->dtype, pl.sk, part, s);
     if (e != hipSuccess) return hip_fail(e, "skinny launch");
     t_last_path = pl.split ? "skinny:split" : "skinny";
+    return GEV2_OK;
+  }
+
+  // ---- small fp32 problems: one launch, no scratch ----
+  if (pl.small_waves > 0) {
+    gev2::SmallArgs a{};
+    gev2::SmallJob& J = a.job[0];
+    J.a = small_op(d->A, ta ? 1 : lda, ta ? lda : 1);
+    J.b = small_op(d->B, tb ? ldb : 1, tb ? 1 : ldb);
+    J.kind = 0;
+    J.rows = static_cast<int>(M); J.cols = static_cast<int>(N); J.red = static_cast<int>(K);
+    J.tiles_c = static_cast<int>((N + 15) / 16);
+    J.tiles = static_cast<int>((M + 15) / 16) * J.tiles_c;
+    J.scale = d->alpha;
+    J.out = static_cast<float*>(d->Y); J.ldo = ldy;
+    a.njobs = 1; a.fwd = 1;
+    a.act = d->act; a.slope = d->leaky_slope;
+    a.bias = has_bias ? d->bias : nullptr; a.bias_kind = has_bias ? d->bias_kind : GEV2_BIAS_NONE;
+    a.Z = static_cast<float*>(d->Z); a.ldz = ldz;
+    hipError_t e = gev2::launch_small(a, pl.small_waves, s);
+    if (e != hipSuccess) return hip_fail(e, "small launch");
+    t_last_path = "small";
     return GEV2_OK;
   }
 
@@ -547,7 +596,27 @@ struct BwdScratch {
   // dx_ks slices of dx_kc (the last dx_kc_last), partials [dx_ks][M][K] fp32
   int dx_ks{0};
   int64_t dx_kc{0}, dx_kc_last{0}, dx_bytes{0};
+  // the whole backward in one launch of the small kernel, with this many
+  // waves per workgroup (0: not taken); needs no scratch
+  int small_waves{0};
 };
+
+// Small fp32 backward in one launch (dX and dW tiles with dY' formed while
+// loading, then the PerN dBias columns): no gC, no PerM / Scalar dBias, at most
+// 2048 output tiles, 65536 dY' elements, reductions of at most 2048 and 2^26
+// multiply-adds.
+int small_bwd_waves(const gev2_gemm_bwd_desc* d) {
+  const int64_t M = d->M, N = d->N, K = d->K;
+  const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
+  if (d->dtype != GEV2_F32 || d->batch != 1 || d->gC || env_int("GEV2_NO_SMALL", 0) != 0) return 0;
+  if (want_bias && d->bias_kind != GEV2_BIAS_PER_N) return 0;
+  if (!d->gA && !d->gB && !want_bias) return 0;
+  const int64_t tiles = (d->gA ? ((M + 15) / 16) * ((K + 15) / 16) : 0) +
+                        (d->gB ? ((K + 15) / 16) * ((N + 15) / 16) : 0);
+  if (tiles > 2048 || M * N > 65536 || M > 2048 || N > 2048 || static_cast<double>(M) * N * K > 67108864.0)
+    return 0;
+  return small_waves_for(std::max<int64_t>(d->gA ? N : 0, d->gB ? M : 0));
+}
 
 int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
 
@@ -561,6 +630,8 @@ BwdScratch bwd_scratch(const gev2_gemm_bwd_desc* d) {
   const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
   const bool linear = d->act == GEV2_ACT_NONE || d->act == GEV2_ACT_RELU || d->act == GEV2_ACT_LEAKY_RELU;
   const double work = static_cast<double>(M) * N * K * batch;
+  r.small_waves = small_bwd_waves(d);
+  if (r.small_waves > 0) return r;
   r.materialise = (!linear || work >= (1u << 30)) && (d->gA || d->gB) && env_int("GEV2_FUSED_BWD", 0) == 0;
   if (!r.materialise) {
     // small fp32 problems: dX (few 64x64 tiles, long reduction over N) split
@@ -625,6 +696,7 @@ int64_t gev2_gemm_bwd_workspace_size(const gev2_gemm_bwd_desc* d) {
 
 int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   t_last_error.clear();
+  t_last_path = "bwd";
   if (!d) return fail(GEV2_INVALID_ARGUMENT, "null descriptor");
   int st = check_common(d->dtype, d->act, d->bias_kind, d->M, d->N, d->K, d->batch);
   if (st != GEV2_OK) return st;
@@ -661,6 +733,44 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
   bool fused = true;
   bool bias_done = false;
   const BwdScratch sc = bwd_scratch(d);
+  if (sc.small_waves > 0) {
+    // the whole backward in one launch: dX = alpha dY' B^T, dW = alpha A^T dY',
+    // dBias = column sums of dY', with dY' = dY (.) act'(Z) formed on load
+    gev2::SmallArgs a{};
+    const auto* gy = static_cast<const float*>(d->gY);
+    const auto* z = static_cast<const float*>(d->Z);
+    if (d->gA) {
+      gev2::SmallJob& J = a.job[a.njobs++];
+      J.a = small_op(gy, ldgy, 1, z, ldz, 1);   // (m, n)
+      J.b = small_op(d->B, ldb, 1);             // (k, n) of B [K,N]
+      J.kind = 1;
+      J.rows = static_cast<int>(M); J.cols = static_cast<int>(K); J.red = static_cast<int>(N);
+      J.tiles_c = static_cast<int>((K + 15) / 16);
+      J.tiles = static_cast<int>((M + 15) / 16) * J.tiles_c;
+      J.scale = d->alpha;
+      J.out = static_cast<float*>(d->gA); J.ldo = ldga;
+    }
+    if (d->gB) {
+      gev2::SmallJob& J = a.job[a.njobs++];
+      J.a = small_op(d->A, 1, lda);             // (k, m) of A [M,K]
+      J.b = small_op(gy, 1, ldgy, z, 1, ldz);   // (n, m)
+      J.kind = 2;
+      J.rows = static_cast<int>(K); J.cols = static_cast<int>(N); J.red = static_cast<int>(M);
+      J.tiles_c = static_cast<int>((N + 15) / 16);
+      J.tiles = static_cast<int>((K + 15) / 16) * J.tiles_c;
+      J.scale = d->alpha;
+      J.out = static_cast<float*>(d->gB); J.ldo = ldgb;
+    }
+    a.fwd = 0;
+    a.act = d->act; a.slope = d->leaky_slope;
+    a.gY = gy; a.ldgy = ldgy; a.Zin = z; a.ldzin = ldz;
+    a.gbias = want_bias ? d->gBias : nullptr;
+    a.M = static_cast<int>(M); a.N = static_cast<int>(N);
+    hipError_t e = gev2::launch_small(a, sc.small_waves, s);
+    if (e != hipSuccess) return hip_fail(e, "small backward launch");
+    t_last_path = "small";
+    return GEV2_OK;
+  }
   // Where dY' goes: the caller's workspace when it holds dY'; otherwise the
   // per-stream buffer.  Under graph capture without either (nothing is
   // allocated then) the GEMMs apply act' to dY on load instead for none /

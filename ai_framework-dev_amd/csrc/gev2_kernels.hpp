@@ -103,6 +103,45 @@ struct SplitkReduceArgs {
   float* Z; int64_t ldz;
 };
 hipError_t launch_splitk_reduce(const SplitkReduceArgs& a, hipStream_t s);
+
+// Small fp32 problems in one launch (gemm_small.hip).  Operand element (i, k)
+// (i: output row for the left operand, output column for the right one; k:
+// reduction index) is p[i * rs + k * ks], times act'(z[i * zrs + k * zks])
+// when z is set (dY' formed while loading).  vec: ks = 1 (and zks = 1), p
+// (and z) 16-byte aligned, rs (and zrs) multiples of 4, so that four
+// consecutive k from a multiple of 4 are one 16-byte load.
+struct SmallOperand {
+  const float* p; int64_t rs, ks;
+  const float* z; int64_t zrs, zks;
+  int vec;
+};
+// out[rows, cols] (leading dimension ldo) = scale * sum_k a(row, k) b(col, k);
+// kind 0: forward, 1: dX (a is dY'), 2: dW (b is dY')
+struct SmallJob {
+  SmallOperand a, b;
+  int kind;
+  int rows, cols, red;
+  int tiles_c, tiles;   // 16x16 tiles along cols, in all
+  float scale;
+  float* out; int64_t ldo;
+};
+// fwd: job 0 is the forward, Z = scale * acc + bias, out = act(Z).
+// Otherwise jobs 0 and 1 (dX, dW) store scale * acc, and when gbias is set
+// further workgroups (64 columns each) sum dY' = gY (.) act'(Zin) over the M
+// rows of each of the N columns (PerN dBias).
+struct SmallArgs {
+  SmallJob job[2];
+  int njobs, fwd;
+  int act; float slope;
+  const float* bias; int bias_kind;
+  float* Z; int64_t ldz;
+  const float* gY; int64_t ldgy;
+  const float* Zin; int64_t ldzin;
+  float* gbias;
+  int M, N;
+};
+// waves per workgroup: 4 or 16
+hipError_t launch_small(const SmallArgs& a, int waves, hipStream_t s);
 hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
                                   float* gbias, int64_t sGbias, int batch, hipStream_t s);
 

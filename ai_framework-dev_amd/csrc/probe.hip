@@ -57,7 +57,45 @@ probe_mfma_kernel(int random_operands, int iters) {
   if (s == 1234.5f) gev2_probe_sink[0] = s;   // keeps the MFMAs live; never true in practice
 }
 
+// Streaming read: workgroup w reads chunks w, w + grid, ... of
+// 256 threads x U x 16 bytes, every thread with its U 16-byte loads in flight
+// at once, and folds them into one word.
+template <int U>
+__global__ void __launch_bounds__(256) probe_read_kernel(const u32x4* __restrict__ src, int64_t chunks) {
+  uint32_t x = 0u;
+  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const u32x4* p = src + c * (256 * U) + threadIdx.x;
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + u * 256);
+#pragma unroll
+    for (int u = 0; u < U; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  if (x == 0x9e3779b9u) gev2_probe_sink[0] = static_cast<float>(x);   // keeps the loads live
+}
+
 }  // namespace gev2
+
+extern "C" int gev2_probe_hbm_read(const void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll,
+                                   void* stream) {
+  const size_t chunk = static_cast<size_t>(256) * 16 * static_cast<size_t>(unroll);
+  if (!buf || sets < 1 || reps < 1 || workgroups < 1) return GEV2_INVALID_ARGUMENT;
+  if (unroll != 8 && unroll != 16 && unroll != 32) return GEV2_INVALID_ARGUMENT;
+  if (bytes == 0 || bytes % chunk != 0 || (reinterpret_cast<uintptr_t>(buf) & 15u) != 0) return GEV2_INVALID_ARGUMENT;
+  const int64_t chunks = static_cast<int64_t>(bytes / chunk);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int r = 0; r < reps; ++r) {
+    const auto* src = reinterpret_cast<const gev2::u32x4*>(static_cast<const char*>(buf) + (r % sets) * bytes);
+    if (unroll == 8)
+      hipLaunchKernelGGL(gev2::probe_read_kernel<8>, dim3(workgroups), dim3(256), 0, s, src, chunks);
+    else if (unroll == 16)
+      hipLaunchKernelGGL(gev2::probe_read_kernel<16>, dim3(workgroups), dim3(256), 0, s, src, chunks);
+    else
+      hipLaunchKernelGGL(gev2::probe_read_kernel<32>, dim3(workgroups), dim3(256), 0, s, src, chunks);
+    if (hipGetLastError() != hipSuccess) return GEV2_HIP_ERROR;
+  }
+  return GEV2_OK;
+}
 
 extern "C" int gev2_probe_mfma_bf16(int random_operands, int iters, void* stream) {
   if (iters < 1) return GEV2_INVALID_ARGUMENT;

@@ -407,8 +407,11 @@ def skinny_cfg(ctx, iters, sets=10):
     path = capi.last_path()
     ms = ctx.time_repeat(fds, iters, "fwd")
     byt = (M * K + K * N + M * N) * 2 + N * 4
-    return {"fwd_us": ms * 1e3, "gbps": byt / (ms * 1e-3) / 1e9,
-            "frac_hbm": byt / (ms * 1e-3) / 1e9 / PEAK_HBM, "path": path}
+    probe = hbm_read_ceiling(ctx)
+    gbps = byt / (ms * 1e-3) / 1e9
+    return {"fwd_us": ms * 1e3, "gbps": gbps, "frac_hbm": gbps / PEAK_HBM, "path": path,
+            "read_probe_gbps": probe["gbps"], "read_probe_us": probe["us"],
+            "frac_of_read_probe": gbps / probe["gbps"]}
 
 
 def cpu_baseline(M=4096, N=4096, K=4096, min_seconds=10.0, max_reps=200):
@@ -527,6 +530,21 @@ def mfma_ceiling(ctx, iters=4096):
                                             "probe"), 10, warmup=2)
         out[name] = round(flop / (ms * 1e-3) / 1e12, 1)
     return out
+
+
+def hbm_read_ceiling(ctx, nbytes=32 << 20, sets=10, reps=50):
+    """Rate of the fastest plain streaming read of nbytes on this part
+    (gev2_probe_hbm_read: 2048 workgroups, eight 16-byte loads in flight per
+    thread, the best of a sweep over 256-4096 workgroups and 8-32 loads),
+    rotating `sets` buffers past the MALL: the ceiling for a kernel that must
+    read that many bytes once."""
+    capi = ctx.capi
+    lib = capi.lib()
+    buf = ctx.empty(nbytes * sets)
+    capi.check(lib.gev2_memset(buf, 0, nbytes * sets), "memset")
+    ms = ctx.time_ms(lambda: capi.check(lib.gev2_probe_hbm_read(buf, nbytes, sets, reps, 2048, 8, ctx.stream.ptr),
+                                        "read probe"), 3, warmup=1) / reps
+    return {"bytes": nbytes, "us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
 def kernel_name(path):

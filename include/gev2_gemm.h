@@ -119,8 +119,11 @@ typedef struct gev2_gemm_fwd_desc {
  * Replaces GemmCudaBackward (launcher.cu:279-383 + regemm_backward.cu:151-301).
  * gBias is overwritten (the reference zero-fills it first, :190-197).
  * gZ is either formed while the GEMM kernels load their operands (act none /
- * ReLU / LeakyReLU on problems below 2^30 multiply-adds) or written once to
- * `workspace` by a pass that also sums dBias, after which the two GEMMs read it.
+ * ReLU / LeakyReLU on problems below 2^30 multiply-adds, and every activation
+ * in the one-launch fp32 backward of small problems: no gC, no PerM / Scalar
+ * dBias, at most 2048 16x16 output tiles and 65536 gZ elements) or written
+ * once to `workspace` by a pass that also sums dBias, after which the two GEMMs
+ * read it.
  */
 typedef struct gev2_gemm_bwd_desc {
   int32_t dtype;
@@ -412,13 +415,27 @@ int gev2_gemm_bwd_repeat(const gev2_gemm_bwd_desc* descs, int n_descs, int reps,
  */
 int gev2_probe_mfma_bf16(int random_operands, int iters, void* stream);
 
+/*
+ * Measurement helper (no counterpart in the reference): `reps` back-to-back
+ * launches, launch r reading the `bytes` at buf + (r % sets) * bytes (buf
+ * 16-byte aligned, bytes a multiple of 4096 * unroll) with `workgroups`
+ * 256-thread workgroups, each thread keeping `unroll` (8, 16 or 32) 16-byte
+ * loads in flight; the data is discarded.  Timed with events on `stream`,
+ * with sets * bytes larger than the 256 MB MALL, it gives the rate at which
+ * this part streams a read of that size from HBM: the ceiling for the
+ * bandwidth-bound forms (skinny M, the SDPA products).
+ */
+int gev2_probe_hbm_read(const void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll,
+                        void* stream);
+
 int gev2_abi_version(void);
 const char* gev2_status_string(int status);
 /* Message for the last failing call on this thread ("" if none). */
 const char* gev2_last_error(void);
 /* Name of the kernel family the last gev2_gemm_fwd on this thread used
- * ("dl:<cfg>", "tile:<cfg>", "skinny:split", "skinny"), for tests and
- * profiling. */
+ * ("dl:<cfg>", "tile:<cfg>", "tile:splitk", "skinny:split", "skinny",
+ * "small"), or after a gev2_gemm_bwd "small" (the one-launch backward) or
+ * "bwd" (any other), for tests and profiling. */
 const char* gev2_last_path(void);
 
 /*

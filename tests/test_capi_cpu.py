@@ -122,7 +122,7 @@ def _bwd_ws(capi, **kw):
     return capi.lib().gev2_gemm_bwd_workspace_size(ctypes.byref(d))
 
 
-def test_backward_workspace_size(capi):
+def test_backward_workspace_size(capi, monkeypatch):
     """The backward's scratch: none when dY' is formed while loading (piecewise-linear act on a
     problem under 2^30 multiply-adds); otherwise dY' (batch*M*N elements).  A PerN dBias on
     aligned rows is summed into ceil(M/64)*N fp32 partials parked in the dX output when it is
@@ -139,11 +139,18 @@ def test_backward_workspace_size(capi):
     assert _bwd_ws(capi, **pern, gY=(1 << 28) + 2, **big) == 4096 * 4096 * 2  # unaligned: no partials
     assert _bwd_ws(capi, act="tanh", M=3, N=10) == 3 * 10 * 2          # dY' only
     assert _bwd_ws(capi, act="gelu", gA=0, gB=0) == 0                  # nothing to multiply
-    # small fp32 problem, dY' formed while loading: dX split over N into fp32 partials
-    # (C1: 8 slices of 32 over N = 256, 64 x 784 partial outputs each)
+    # small fp32 problem: the whole backward in one launch of the small kernel, act' of every
+    # kind formed while loading, no scratch
     c1 = dict(dtype=0, M=64, N=256, K=784)
+    assert _bwd_ws(capi, **c1) == 0
+    assert _bwd_ws(capi, **c1, act="gelu") == 0
+    assert _bwd_ws(capi, **c1, act="gelu", gC=1 << 34, beta=1.0) == 64 * 256 * 4   # gC: not small
+    # without the small kernel: dY' formed while loading, dX split over N into fp32 partials
+    # (C1: 8 slices of 32 over N = 256, 64 x 784 partial outputs each)
+    monkeypatch.setenv("GEV2_NO_SMALL", "1")
     assert _bwd_ws(capi, **c1) == 8 * 64 * 784 * 4
     assert _bwd_ws(capi, **c1, gA=0) == 0                              # no dX: no split
+    monkeypatch.delenv("GEV2_NO_SMALL")
     assert _bwd_ws(capi, dtype=7) == -1
 
 

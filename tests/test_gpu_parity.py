@@ -375,6 +375,7 @@ def test_fp32_splitk(gpu, case, monkeypatch):
     a caller workspace (same slices, same order), and equal to the unsplit path within the bound."""
     capi = gpu
     M, N, K, act, bk = case
+    monkeypatch.setenv("GEV2_NO_SMALL", "1")        # these shapes otherwise take the small kernel
     path = _check_fwd(capi, M, N, K, F32, act, bk, seed=700 + M, alpha=0.5)
     assert path == "tile:splitk", path
     X, W, b = make_fwd_inputs(701, M, N, K, F32, bk)
@@ -414,6 +415,7 @@ def test_fp32_backward_dx_splitk(gpu, case, monkeypatch):
     and within twice that bound of the unsplit launch."""
     capi = gpu
     M, N, K, act = case
+    monkeypatch.setenv("GEV2_NO_SMALL", "1")        # these shapes otherwise take the small kernel
     X, W, b = make_fwd_inputs(810 + M, M, N, K, F32, O.BIAS_PERN)
     gY = np.random.default_rng(811 + M).standard_normal((M, N)).astype(np.float32)
     Z = np.random.default_rng(812 + M).standard_normal((M, N)).astype(np.float32)

@@ -98,6 +98,7 @@ def test_tile_variants_exact_f32(gpu, monkeypatch, cfg, case, kernel):
     monkeypatch.setenv("GEV2_TILE_CFG", str(cfg))
     monkeypatch.setenv("GEV2_DL", "1" if kernel == "dl" else "0")
     monkeypatch.setenv("GEV2_NO_SPLITK", "1")        # one launch over all of K
+    monkeypatch.setenv("GEV2_NO_SMALL", "1")         # the tile kernels, not the small one
     layout, M, N, K, pad = case
     Y, Z, Yr, Zr, path = _run(capi, layout, M, N, K, pad, F32, O.BIAS_PERN, "relu", seed=cfg * 11 + M)
     assert path == (f"dl:{CFGS_F32[cfg]}" if kernel == "dl" else f"tile:{PIPE_NAME.get(cfg, CFGS_F32[cfg])}"), path
