@@ -475,6 +475,7 @@ int gemm_fwd_run(const gev2_gemm_fwd_desc* d, void* stream, void* fixed, int64_t
     J.rows = static_cast<int>(M); J.cols = static_cast<int>(N); J.red = static_cast<int>(K);
     J.tiles_c = static_cast<int>((N + 15) / 16);
     J.tiles = static_cast<int>((M + 15) / 16) * J.tiles_c;
+    J.wgs = J.tiles;
     J.scale = d->alpha;
     J.out = static_cast<float*>(d->Y); J.ldo = ldy;
     a.njobs = 1; a.fwd = 1;
@@ -605,17 +606,27 @@ struct BwdScratch {
 // loading, then the PerN dBias columns): no gC, no PerM / Scalar dBias, at most
 // 2048 output tiles, 65536 dY' elements, reductions of at most 2048 and 2^26
 // multiply-adds.
+// A job whose reduction is at most kSmallOwnRed gives each wave a tile of its
+// own; longer ones split each tile's reduction over the workgroup's waves.
+constexpr int64_t kSmallOwnRed = 64;
+
 int small_bwd_waves(const gev2_gemm_bwd_desc* d) {
   const int64_t M = d->M, N = d->N, K = d->K;
   const bool want_bias = d->gBias && d->bias_kind != GEV2_BIAS_NONE;
   if (d->dtype != GEV2_F32 || d->batch != 1 || d->gC || env_int("GEV2_NO_SMALL", 0) != 0) return 0;
   if (want_bias && d->bias_kind != GEV2_BIAS_PER_N) return 0;
   if (!d->gA && !d->gB && !want_bias) return 0;
+  if (M * N > 65536 || M > 2048 || N > 2048 || static_cast<double>(M) * N * K > 67108864.0) return 0;
+  // waves from the longest split reduction (dX: N, dW: M)
+  int64_t split_red = 0;
+  if (d->gA && N > kSmallOwnRed) split_red = std::max(split_red, N);
+  if (d->gB && M > kSmallOwnRed) split_red = std::max(split_red, M);
+  const int w = small_waves_for(split_red);
+  // at most 2048 output tiles in all: past that (the rank-8 dW of an RNN step,
+  // 6144 tiles) one launch measured no faster than the multi-launch path
   const int64_t tiles = (d->gA ? ((M + 15) / 16) * ((K + 15) / 16) : 0) +
                         (d->gB ? ((K + 15) / 16) * ((N + 15) / 16) : 0);
-  if (tiles > 2048 || M * N > 65536 || M > 2048 || N > 2048 || static_cast<double>(M) * N * K > 67108864.0)
-    return 0;
-  return small_waves_for(std::max<int64_t>(d->gA ? N : 0, d->gB ? M : 0));
+  return tiles <= 2048 ? w : 0;
 }
 
 int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
@@ -747,6 +758,8 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       J.rows = static_cast<int>(M); J.cols = static_cast<int>(K); J.red = static_cast<int>(N);
       J.tiles_c = static_cast<int>((K + 15) / 16);
       J.tiles = static_cast<int>((M + 15) / 16) * J.tiles_c;
+      J.own = N <= kSmallOwnRed;
+      J.wgs = J.own ? (J.tiles + sc.small_waves - 1) / sc.small_waves : J.tiles;
       J.scale = d->alpha;
       J.out = static_cast<float*>(d->gA); J.ldo = ldga;
     }
@@ -758,6 +771,8 @@ int gev2_gemm_bwd(const gev2_gemm_bwd_desc* d, void* stream) {
       J.rows = static_cast<int>(K); J.cols = static_cast<int>(N); J.red = static_cast<int>(M);
       J.tiles_c = static_cast<int>((N + 15) / 16);
       J.tiles = static_cast<int>((K + 15) / 16) * J.tiles_c;
+      J.own = M <= kSmallOwnRed;
+      J.wgs = J.own ? (J.tiles + sc.small_waves - 1) / sc.small_waves : J.tiles;
       J.scale = d->alpha;
       J.out = static_cast<float*>(d->gB); J.ldo = ldgb;
     }

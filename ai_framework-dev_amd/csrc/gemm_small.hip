@@ -16,7 +16,8 @@
 //     16-byte loads where the operand is contiguous along the reduction) and
 //     accumulate with v_mfma_f32_16x16x4f32;
 //   - the W partial tiles meet in LDS and are added in wave order, then the
-//     epilogue writes the tile;
+//     epilogue writes the tile; a backward job with a reduction of at most 64
+//     (C1's dW, a rank-8 dW) instead gives each wave a tile of its own;
 //   - in the backward, workgroups past the dX and dW tiles each sum 64
 //     columns of dY' over the rows, split over their waves (PerN dBias).
 //
@@ -106,6 +107,40 @@ __device__ __forceinline__ void small_tile(const SmallArgs& p, const SmallJob& J
   }
 }
 
+// Short reductions (at most 64): each wave of workgroup g owns tile W g + wave
+// and runs the whole reduction itself; no LDS, no barrier.
+template <int W, bool AV, bool BV, bool AZ, bool BZ, int ACT>
+__device__ __forceinline__ void small_tile_own(const SmallArgs& p, const SmallJob& J, int g) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int t = g * W + wave;
+  if (t >= J.tiles) return;
+  const int tr = t / J.tiles_c, tc = t - tr * J.tiles_c;
+  const int r = tr * 16 + (lane & 15), c = tc * 16 + (lane & 15), kq = lane >> 4;
+  const bool rin = r < J.rows, cin = c < J.cols;
+  const int blocks = (J.red + 15) >> 4;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < blocks; j0 += 4) {
+    f32x4_t av[4], bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k0 = 16 * (j0 + u) + 4 * kq;
+      av[u] = rin ? small_load4<AV, AZ, ACT>(J.a, r, k0, J.red, p.slope) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      bv[u] = cin ? small_load4<BV, BZ, ACT>(J.b, c, k0, J.red, p.slope) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][e], bv[u][e], acc, 0, 0, 0);
+  }
+  const int col = tc * 16 + (lane & 15);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int row = tr * 16 + 4 * (lane >> 4) + v;
+    if (row < J.rows && col < J.cols) J.out[(int64_t)row * J.ldo + col] = J.scale == 1.f ? acc[v] : J.scale * acc[v];
+  }
+}
+
 // PerN dBias: workgroup b sums columns 64 b + lane; wave w adds rows
 // w, w + W, ... in order (16 loads of each array in flight), then wave 0 adds
 // the W wave sums in order.
@@ -151,16 +186,21 @@ __global__ void __launch_bounds__(W * 64) small_fwd_kernel(SmallArgs p) {
 // along the reduction.
 template <int W, int ACT, bool GAV>
 __device__ __forceinline__ void small_bwd_job(const SmallArgs& p, const SmallJob& J, int t, float* red) {
-  if (J.kind == 1) small_tile<W, GAV, GAV, true, false, ACT, false>(p, J, t, red);
-  else small_tile<W, false, false, false, true, ACT, false>(p, J, t, red);
+  if (J.kind == 1) {
+    if (J.own) small_tile_own<W, GAV, GAV, true, false, ACT>(p, J, t);
+    else small_tile<W, GAV, GAV, true, false, ACT, false>(p, J, t, red);
+  } else {
+    if (J.own) small_tile_own<W, false, false, false, true, ACT>(p, J, t);
+    else small_tile<W, false, false, false, true, ACT, false>(p, J, t, red);
+  }
 }
 
 template <int W, int ACT, bool GAV>
 __global__ void __launch_bounds__(W * 64) small_bwd_kernel(SmallArgs p) {
   __shared__ float red[W * 256];
   const int t = blockIdx.x;
-  const int t0 = p.njobs > 0 ? p.job[0].tiles : 0;
-  const int t1 = p.njobs > 1 ? p.job[1].tiles : 0;
+  const int t0 = p.njobs > 0 ? p.job[0].wgs : 0;
+  const int t1 = p.njobs > 1 ? p.job[1].wgs : 0;
   if (t < t0) small_bwd_job<W, ACT, GAV>(p, p.job[0], t, red);
   else if (t < t0 + t1) small_bwd_job<W, ACT, GAV>(p, p.job[1], t - t0, red);
   else small_dbias<W, ACT>(p, t - t0 - t1, red);
@@ -196,7 +236,12 @@ static hipError_t launch_small_w(const SmallArgs& a, int wgs, hipStream_t s) {
 
 hipError_t launch_small(const SmallArgs& a, int waves, hipStream_t s) {
   int wgs = 0;
-  for (int j = 0; j < a.njobs; ++j) wgs += a.job[j].tiles;
+  for (int j = 0; j < a.njobs; ++j) {
+    if (a.job[j].wgs != (a.job[j].own ? (a.job[j].tiles + waves - 1) / waves : a.job[j].tiles) ||
+        (a.fwd && a.job[j].own))
+      return hipErrorInvalidValue;
+    wgs += a.job[j].wgs;
+  }
   if (!a.fwd && a.gbias) wgs += (a.N + 63) / 64;
   if (wgs <= 0) return hipSuccess;
   return waves == 16 ? launch_small_w<16>(a, wgs, s) : launch_small_w<4>(a, wgs, s);

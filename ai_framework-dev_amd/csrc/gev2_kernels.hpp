@@ -116,12 +116,15 @@ struct SmallOperand {
   int vec;
 };
 // out[rows, cols] (leading dimension ldo) = scale * sum_k a(row, k) b(col, k);
-// kind 0: forward, 1: dX (a is dY'), 2: dW (b is dY')
+// kind 0: forward, 1: dX (a is dY'), 2: dW (b is dY').  own (backward only):
+// each wave takes a whole tile (wgs = ceil(tiles / waves)); otherwise the
+// waves of a workgroup split one tile's reduction (wgs = tiles).
 struct SmallJob {
   SmallOperand a, b;
-  int kind;
+  int kind, own;
   int rows, cols, red;
   int tiles_c, tiles;   // 16x16 tiles along cols, in all
+  int wgs;
   float scale;
   float* out; int64_t ldo;
 };

@@ -151,6 +151,8 @@ BWD_CASES = [
     (130, 200, 64, "leakyrelu", O.BIAS_PERN, ("gB",), 1.0),                # dW alone
     (700, 90, 20, "none", O.BIAS_PERN, ("gA", "gB", "gBias"), 1.0),        # long dW reduction
     (5, 384, 200, "relu", O.BIAS_PERN, ("gBias",), 1.0),                   # dBias alone
+    (8, 512, 600, "tanh", O.BIAS_PERN, ("gA", "gB", "gBias"), 1.0),       # rank-8 dW: a tile per wave
+    (64, 40, 300, "gelu", O.BIAS_NONE, ("gA", "gB"), 1.0),                 # both reductions short
 ]
 
 
