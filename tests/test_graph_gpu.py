@@ -48,10 +48,9 @@ def test_dense_step_graph_replays(mods, dtype, act, warmup):
     if warmup:
         step(x, gy, cap_bufs)                   # eager warm-up on the capture stream
         stream.synchronize()
-    # The graph holds the eager call's kernels when the warm-up left the stream's scratch
-    # in place (or none is needed); the fp32 forward here is small enough to split K, which
-    # needs scratch, so without the warm-up its graph holds the plain tile kernel.
-    exact = warmup or dtype != "float32"
+    # The graph holds the eager call's kernels: the 16-bit paths here need no scratch, and the
+    # fp32 layer is small enough for the one-launch kernels, which need none either.
+    exact = True
     with capture_stream(stream) as cap:
         step(x, gy, cap_bufs)
     gexec = cap.graph.instantiate()
@@ -177,6 +176,48 @@ def test_capture_without_workspace_then_larger_eager_call(mods):
     assert np.all(np.abs(o["gA"] - ref["gA"]) <= 1.01 * N * U_ACC * (aG @ Wt) + u * np.abs(ref["gA"]) + 1e-7)
     assert np.all(np.abs(o["gB"] - ref["gB"]) <= 1.01 * M * U_ACC * (Xt @ aG) + u * np.abs(ref["gB"]) + 1e-7)
     assert np.all(np.abs(o["gb"] - ref["gBias"]) <= 1.01 * M * U_ACC * aG.sum(0) + 1e-7)
+
+
+def test_capture_small_fp32_gelu_without_workspace(mods):
+    """A small fp32 GELU forward + backward (C1's shape) recorded with no workspace and no
+    warm-up: the one-launch kernels form act' while loading and need no scratch, so nothing is
+    refused or allocated, and every replay equals the eager calls bit for bit."""
+    import ctypes
+    from gemm_helpers import F32, Dev
+    capture_stream, _, capi, _ = mods
+    L = capi.lib()
+    stream = capi.Stream()
+    dev = Dev(capi)
+    try:
+        M, N, K = 64, 256, 784
+        _, p, fwd, bwd = _fwd_bwd_descs(capi, dev, F32, M, N, K, "gelu", 75)
+        assert capi.fwd_workspace_size(dtype=F32, M=M, N=N, K=K, A=p["X"], B=p["W"], Y=p["Y"]) == 0
+        assert L.gev2_gemm_bwd_workspace_size(ctypes.byref(bwd)) == 0
+        with capture_stream(stream) as cap:
+            capi.check(L.gev2_gemm_fwd(ctypes.byref(fwd), stream.ptr), "captured fwd")
+            capi.check(L.gev2_gemm_bwd(ctypes.byref(bwd), stream.ptr), "captured bwd")
+        gexec = cap.graph.instantiate()
+        keys = (("Y", (M, N)), ("Z", (M, N)), ("gA", (M, K)), ("gB", (K, N)), ("gb", (N,)))
+        try:
+            replays = []
+            for _ in range(3):
+                for k, _shape in keys:
+                    next(x for x in dev.bufs if x.ptr == p[k]).fill_bytes(0x7f)
+                gexec.launch(stream)
+                stream.synchronize()
+                replays.append({k: dev.get_f32(p[k], shape) for k, shape in keys})
+        finally:
+            gexec.close()
+        capi.check(L.gev2_gemm_fwd(ctypes.byref(fwd), stream.ptr), "eager fwd")
+        capi.check(L.gev2_gemm_bwd(ctypes.byref(bwd), stream.ptr), "eager bwd")
+        stream.synchronize()
+        eager = {k: dev.get_f32(p[k], shape) for k, shape in keys}
+    finally:
+        dev.close()
+        stream.destroy()
+    for r in replays:
+        for k, _shape in keys:
+            np.testing.assert_array_equal(r[k], eager[k], err_msg=k)
 
 
 def test_capture_refuses_transcendental_backward_without_workspace(mods):
