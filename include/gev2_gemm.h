@@ -152,7 +152,8 @@ typedef struct gev2_gemm_bwd_desc {
    * needed.  NULL or too small for dY': the library uses a buffer it
    * allocates once per (device, stream) and keeps, or, while the stream is
    * being captured, forms dY' while loading instead (none / ReLU / LeakyReLU;
-   * other activations return GEV2_MISSING_INPUT then).  Plays the role of the
+   * other activations return GEV2_MISSING_INPUT then).  The one-launch
+   * backward of small fp32 problems needs no workspace for any activation.  Plays the role of the
    * reference's GemmWorkspace::scratch (gemm/api.hpp:97-104). */
   void* workspace; int64_t workspace_bytes;
 } gev2_gemm_bwd_desc;
