@@ -74,7 +74,37 @@ __global__ void __launch_bounds__(256) probe_read_kernel(const u32x4* __restrict
   if (x == 0x9e3779b9u) gev2_probe_sink[0] = static_cast<float>(x);   // keeps the loads live
 }
 
+// Streaming write: workgroup w writes chunks w, w + grid, ... of
+// 256 threads x U x 16 bytes with 16-byte vector stores.
+template <int U>
+__global__ void __launch_bounds__(256) probe_write_kernel(u32x4* __restrict__ dst, int64_t chunks) {
+  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+    u32x4* p = dst + c * (256 * U) + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < U; ++u) p[u * 256] = u32x4{static_cast<uint32_t>(c), static_cast<uint32_t>(u), 0u, 0u};
+  }
+}
+
 }  // namespace gev2
+
+extern "C" int gev2_probe_hbm_write(void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll,
+                                    void* stream) {
+  const size_t chunk = static_cast<size_t>(256) * 16 * static_cast<size_t>(unroll);
+  if (!buf || sets < 1 || reps < 1 || workgroups < 1) return GEV2_INVALID_ARGUMENT;
+  if (unroll != 8 && unroll != 16) return GEV2_INVALID_ARGUMENT;
+  if (bytes == 0 || bytes % chunk != 0 || (reinterpret_cast<uintptr_t>(buf) & 15u) != 0) return GEV2_INVALID_ARGUMENT;
+  const int64_t chunks = static_cast<int64_t>(bytes / chunk);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int r = 0; r < reps; ++r) {
+    auto* dst = reinterpret_cast<gev2::u32x4*>(static_cast<char*>(buf) + (r % sets) * bytes);
+    if (unroll == 8)
+      hipLaunchKernelGGL(gev2::probe_write_kernel<8>, dim3(workgroups), dim3(256), 0, s, dst, chunks);
+    else
+      hipLaunchKernelGGL(gev2::probe_write_kernel<16>, dim3(workgroups), dim3(256), 0, s, dst, chunks);
+    if (hipGetLastError() != hipSuccess) return GEV2_HIP_ERROR;
+  }
+  return GEV2_OK;
+}
 
 extern "C" int gev2_probe_hbm_read(const void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll,
                                    void* stream) {

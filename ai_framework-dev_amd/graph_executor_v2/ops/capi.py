@@ -26,7 +26,7 @@ EXPORTED = [
     "gev2_memcpy_dtoh", "gev2_memcpy_dtod_async", "gev2_memset", "gev2_stream_create",
     "gev2_stream_destroy", "gev2_stream_synchronize", "gev2_device_synchronize",
     "gev2_event_create", "gev2_event_destroy", "gev2_event_record", "gev2_event_synchronize",
-    "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16", "gev2_probe_hbm_read",
+    "gev2_event_elapsed_ms", "gev2_probe_mfma_bf16", "gev2_probe_hbm_read", "gev2_probe_hbm_write",
     "gev2_conv2d_fwd", "gev2_conv2d_bwd", "gev2_conv2d_last_error",
     "gev2_rnn_fwd", "gev2_rnn_bwd", "gev2_rnn_last_error",
     "gev2_sdpa_fwd", "gev2_sdpa_bwd", "gev2_sdpa_workspace_size", "gev2_sdpa_last_error",
@@ -197,6 +197,7 @@ def lib() -> ctypes.CDLL:
     L.gev2_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
     L.gev2_probe_mfma_bf16.argtypes = [i32, i32, vp]
     L.gev2_probe_hbm_read.argtypes = [vp, sz, i32, i32, i32, i32, vp]
+    L.gev2_probe_hbm_write.argtypes = [vp, sz, i32, i32, i32, i32, vp]
     L.gev2_conv2d_fwd.argtypes = [ctypes.POINTER(Conv2dDesc), vp]
     L.gev2_conv2d_bwd.argtypes = [ctypes.POINTER(Conv2dBwdDesc), vp]
     L.gev2_conv2d_last_error.restype = ctypes.c_char_p

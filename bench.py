@@ -215,7 +215,11 @@ def sdpa_cfg(ctx, dtype, iters, sets=8):
     flop = 2.0 * BH * L * L * D
     byt_qk = (2 * BH * L * D + BH * L * L) * es
     byt_pv = (BH * L * L + 2 * BH * L * D) * es
+    # the plain streaming write of S alone, and read of P alone, on this part
+    wprobe = hbm_write_ceiling(ctx, nbytes=BH * L * L * es)
+    rprobe = hbm_read_ceiling(ctx, nbytes=BH * L * L * es)
     return {"qk_us": qk_ms * 1e3, "pv_us": pv_ms * 1e3,
+            "s_write_probe_us": wprobe["us"], "p_read_probe_us": rprobe["us"],
             "qk_gbps": byt_qk / (qk_ms * 1e-3) / 1e9, "pv_gbps": byt_pv / (pv_ms * 1e-3) / 1e9,
             "qk_frac_hbm": byt_qk / (qk_ms * 1e-3) / 1e9 / PEAK_HBM,
             "pv_frac_hbm": byt_pv / (pv_ms * 1e-3) / 1e9 / PEAK_HBM,
@@ -544,6 +548,19 @@ def hbm_read_ceiling(ctx, nbytes=32 << 20, sets=10, reps=50):
     capi.check(lib.gev2_memset(buf, 0, nbytes * sets), "memset")
     ms = ctx.time_ms(lambda: capi.check(lib.gev2_probe_hbm_read(buf, nbytes, sets, reps, 2048, 8, ctx.stream.ptr),
                                         "read probe"), 3, warmup=1) / reps
+    return {"bytes": nbytes, "us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
+def hbm_write_ceiling(ctx, nbytes=32 << 20, sets=10, reps=50):
+    """Rate of the fastest plain streaming write of nbytes on this part
+    (gev2_probe_hbm_write: 512 workgroups, sixteen 16-byte stores per thread,
+    the best of a sweep over 512-4096 workgroups and 4-16 stores), rotating
+    `sets` buffers: the ceiling for a kernel that must write that many bytes."""
+    capi = ctx.capi
+    lib = capi.lib()
+    buf = ctx.empty(nbytes * sets)
+    ms = ctx.time_ms(lambda: capi.check(lib.gev2_probe_hbm_write(buf, nbytes, sets, reps, 512, 16, ctx.stream.ptr),
+                                        "write probe"), 3, warmup=1) / reps
     return {"bytes": nbytes, "us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
 
 

@@ -429,6 +429,15 @@ int gev2_probe_mfma_bf16(int random_operands, int iters, void* stream);
 int gev2_probe_hbm_read(const void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll,
                         void* stream);
 
+/*
+ * Measurement helper (no counterpart in the reference): as gev2_probe_hbm_read,
+ * but each launch overwrites the `bytes` at buf + (r % sets) * bytes with
+ * 16-byte stores (unroll 8 or 16 per thread): the rate at which this part
+ * streams a write of that size to HBM, the ceiling for store-bound forms such
+ * as the SDPA score product.
+ */
+int gev2_probe_hbm_write(void* buf, size_t bytes, int sets, int reps, int workgroups, int unroll, void* stream);
+
 int gev2_abi_version(void);
 const char* gev2_status_string(int status);
 /* Message for the last failing call on this thread ("" if none). */
