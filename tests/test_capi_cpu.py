@@ -61,6 +61,23 @@ def test_forward_validation_codes(capi):
     assert b"lead" in capi.lib().gev2_last_error() or True
 
 
+def test_probe_argument_checks(capi):
+    """The measurement helpers refuse bad arguments before touching the device."""
+    L = capi.lib()
+    buf = 1 << 20                                     # never dereferenced: every call below is refused
+    nb = 4096 * 8
+    assert L.gev2_probe_hbm_read(None, nb, 1, 1, 256, 8, None) == 4
+    assert L.gev2_probe_hbm_read(buf, nb + 16, 1, 1, 256, 8, None) == 4     # not a whole chunk
+    assert L.gev2_probe_hbm_read(buf, nb, 1, 1, 256, 12, None) == 4        # unroll 8 / 16 / 32
+    assert L.gev2_probe_hbm_read(buf + 8, nb, 1, 1, 256, 8, None) == 4     # 16-byte alignment
+    assert L.gev2_probe_hbm_read(buf, nb, 0, 1, 256, 8, None) == 4
+    assert L.gev2_probe_hbm_write(None, nb, 1, 1, 256, 8, None) == 4
+    assert L.gev2_probe_hbm_write(buf, nb, 1, 1, 256, 32, None) == 4       # unroll 8 / 16
+    assert L.gev2_probe_hbm_write(buf, 0, 1, 1, 256, 8, None) == 4
+    assert L.gev2_probe_hbm_write(buf, nb, 1, 0, 256, 8, None) == 4
+    assert L.gev2_probe_mfma_bf16(1, 0, None) == 4
+
+
 def test_backward_validation_codes(capi):
     import ctypes
     d = capi.BwdDesc()
