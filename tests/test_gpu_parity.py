@@ -70,7 +70,8 @@ def test_forward_shapes(gpu, dtype, shape):
     bias = BIASES[(i + 2 * dtype) % len(BIASES)]
     path = _check_fwd(gpu, M, N, K, dtype, act, bias, seed=1000 + 10 * i + dtype)
     if M <= 16 and K >= 64:
-        assert path.startswith("skinny")
+        # fp32 with K >= 128 takes the one-launch small kernel instead
+        assert path.startswith("skinny") or (dtype == F32 and K >= 128 and path == "small"), path
     elif (K * (4 if dtype == F32 else 2)) % 16:
         assert path.endswith("scalar")
 
