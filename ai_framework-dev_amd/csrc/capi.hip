@@ -313,8 +313,9 @@ bool splitk_slices(int64_t R, int64_t tiles, int64_t* kc_out, int64_t* ks_out) {
   return true;
 }
 
-// fp32 problems too small to occupy the GPU with 64x64 tiles (C1: 4 tiles on
-// 256 CUs, each running K = 784 alone) split K over workgroups: slices of kc
+// fp32 problems too small to occupy the GPU with 64x64 tiles (the 64x256
+// output of a 784-input MLP layer: 4 tiles on 256 CUs, each running K = 784
+// alone) split K over workgroups: slices of kc
 // run as one batched launch into fp32 partials, and a
 // second pass adds the slices in order and applies alpha, bias, Z and act.
 void plan_splitk(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {

@@ -374,8 +374,9 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
 
 // Y = act(alpha * sum_s part[s] + bias), K blocks added in order s = 0, 1, ...
 // One thread per (16-column tile, lane, row pair) of the MFMA result layout,
-// i.e. per 2 rows of one column, so that C5b's 2 MiB of partials spread over
-// 256 single-wave workgroups; every K block's partial is loaded at once.
+// i.e. per 2 rows of one column, so that the 2 MiB of partials of an
+// 8x4096x4096 problem spread over 256 single-wave workgroups; every K block's
+// partial is loaded at once.
 constexpr int kReduceThreads = 64;
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 

@@ -17,7 +17,8 @@
 //     accumulate with v_mfma_f32_16x16x4f32;
 //   - the W partial tiles meet in LDS and are added in wave order, then the
 //     epilogue writes the tile; a backward job with a reduction of at most 64
-//     (C1's dW, a rank-8 dW) instead gives each wave a tile of its own;
+//     (the dW of a 64-row batch, a rank-8 dW) instead gives each wave a
+//     tile of its own;
 //   - in the backward, workgroups past the dX and dW tiles each sum 64
 //     columns of dY' over the rows, split over their waves (PerN dBias).
 //
