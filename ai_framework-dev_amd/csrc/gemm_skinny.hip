@@ -251,14 +251,20 @@ int skinny_split_cols() {
   return c;
 }
 
+// b: the bias term of (m, n), read beforehand (ignored without a bias)
 template <typename T>
-__device__ __forceinline__ void skinny_out(const SkinnyArgs& p, int m, int n, float acc) {
+__device__ __forceinline__ void skinny_out_b(const SkinnyArgs& p, int m, int n, float acc, float b) {
   T* Y = reinterpret_cast<T*>(p.D);
   T* Zo = reinterpret_cast<T*>(p.Zo);
   float pre = p.alpha == 1.f ? acc : p.alpha * acc;
-  if (p.bias) pre += load_bias(p.bias, p.bias_kind, m, n);
+  if (p.bias) pre += b;
   if (Zo) Elem<T>::store1(Zo + (int64_t)m * p.ldzo + n, pre);
   Elem<T>::store1(Y + (int64_t)m * p.ldd + n, act_fwd(pre, p.act, p.slope));
+}
+
+template <typename T>
+__device__ __forceinline__ void skinny_out(const SkinnyArgs& p, int m, int n, float acc) {
+  skinny_out_b<T>(p, m, n, acc, p.bias ? load_bias(p.bias, p.bias_kind, m, n) : 0.f);
 }
 
 // partial of (split, 16-column tile, lane): lanes 0 .. 16*MQ-1 (rows < 4*MQ)
@@ -393,22 +399,37 @@ __global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArg
   const int n = tile * 16 + (lane & 15);
   const int m0 = 4 * (lane >> 4) + 2 * half;
   if (m0 >= p.M || n >= p.N) return;
+  // The bias terms (one vector load each, index chosen without a branch) and
+  // the first 16 K blocks' partials are all in flight together: one memory
+  // round trip for the common K <= 4096.
+  const int bk = p.bias ? p.bias_kind : kBiasNone;
+  float bv[2] = {0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int bi = bk == kBiasPerN ? n : (bk == kBiasPerM ? m0 + r : 0);
+    if (bk != kBiasNone && m0 + r < p.M) bv[r] = p.bias[bi];
+  }
   const f32x2_t* src = reinterpret_cast<const f32x2_t*>(part) + 2 * v + half;
-  f32x2_t sum = src[0];
-  for (int s0 = 1; s0 < nsplit; s0 += 16) {
+  f32x2_t sum = {0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += 16) {
     f32x2_t w[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) w[u] = s0 + u < nsplit ? src[2 * (s0 + u) * per_split] : f32x2_t{0.f, 0.f};
+    for (int u = 0; u < 16; ++u)   // past the last K block: a reload of it, not added (no branch, no copy)
+      w[u] = src[2 * (int64_t)min(s0 + u, nsplit - 1) * per_split];
 #pragma unroll
     for (int u = 0; u < 16; ++u)
       if (s0 + u < nsplit) {
-        sum[0] += w[u][0];
-        sum[1] += w[u][1];
+        if (s0 + u == 0) {
+          sum = w[u];
+        } else {
+          sum[0] += w[u][0];
+          sum[1] += w[u][1];
+        }
       }
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r)
-    if (m0 + r < p.M) skinny_out<T>(p, m0 + r, n, sum[r]);
+    if (m0 + r < p.M) skinny_out_b<T>(p, m0 + r, n, sum[r], bv[r]);
 }
 
 template <typename T, int COLS>
