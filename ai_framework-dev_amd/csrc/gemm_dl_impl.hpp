@@ -251,9 +251,8 @@ gemm_dl_kernel(TileArgs p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
-  int tm, tn;
-  map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int bz = blockIdx.y;
+  int tm, tn, bz;
+  map_tile_batched(p.tiles_m, p.tiles_n, tm, tn, bz);
   const int m0 = tm * BM, n0 = tn * BN;
 
   const i32x4_t rA = rsrc_words(reinterpret_cast<const T*>(p.A) + (int64_t)bz * p.sA);

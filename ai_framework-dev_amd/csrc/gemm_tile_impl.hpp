@@ -35,9 +35,7 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 7
 // dispatched round-robin over the 8 XCDs; remapping gives each XCD a
 // contiguous range of tiles, and the group-of-4 row ordering keeps the tiles
 // an XCD owns compact so its L2 sees A-row and B-column reuse.
-__device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+__device__ __forceinline__ void map_tile_grouped(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int GM = 4;
   const int width = GM * tiles_n;
   const int group = pid / width;
@@ -46,6 +44,34 @@ __device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int&
   const int r = pid - group * width;
   tm = first + r % gsz;
   tn = r / gsz;
+}
+
+__device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  map_tile_grouped(pid, tiles_m, tiles_n, tm, tn);
+}
+
+// Tile and batch slice of this workgroup in a (tiles, batch) grid.  The
+// dispatcher hands workgroups to the 8 XCDs in turn by flattened id (x
+// fastest), so the tiles of one slice would sit on different XCDs and each
+// fetch the slice's shared operand rows past its own L2.  When the grid's
+// workgroup count is a multiple of 8, each XCD instead takes a contiguous run
+// of (slice, tile) items: e.g. the 5 dW tiles of one image of a 3x3
+// convolution's backward (128 x 576 x 3136 per image) read that image's dY'
+// rows through one L2.  One-slice grids keep map_tile's spread.
+__device__ __forceinline__ void map_tile_batched(int tiles_m, int tiles_n, int& tm, int& tn, int& bz) {
+  const int tiles = tiles_m * tiles_n;           // == gridDim.x
+  const int total = tiles * static_cast<int>(gridDim.y);
+  if (gridDim.y > 1 && (total & 7) == 0) {
+    const int L = static_cast<int>(blockIdx.x) + static_cast<int>(blockIdx.y) * tiles;
+    const int g = (L & 7) * (total >> 3) + (L >> 3);
+    bz = g / tiles;
+    map_tile_grouped(g - bz * tiles, tiles_m, tiles_n, tm, tn);
+  } else {
+    bz = blockIdx.y;
+    map_tile(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  }
 }
 
 // Staging of one operand tile: ROWS x BK elements, ROWS along M (or N).
