@@ -292,15 +292,19 @@ gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
   char* wl = lds + wave * WBYTES;
   char* xl = lds + 4 * WBYTES;
 
-  // X: load i fills k-blocks 4i .. 4i+3: lane -> block 4i + lane/16, row m = lane % 16
-  const i32x4_t rX = rsrc_words(p.A);
+  // X: load i fills k-blocks 4i .. 4i+3: lane -> block 4i + lane/16, row m = lane % 16.
+  // A K block lies wholly in A or in A2 (K1 is a multiple of the block).
+  const bool second = p.A2 != nullptr && k0 >= p.K1;
+  const i32x4_t rX = rsrc_words(second ? p.A2 : p.A);
+  const int64_t ldx = second ? p.lda2 : p.lda;
+  const int kx = second ? p.K1 : 0;                          // first X column of the source
   {
     const int m = lane & 15;
 #pragma unroll
     for (int ii = 0; ii < S::kXLoads; ++ii) {
       const int i = S::kXLoads * wave + ii;
       const int k = k0 + 8 * (4 * i + (lane >> 4));
-      const int off = (m < p.M && k < p.K) ? static_cast<int>(((int64_t)m * p.lda + k) * sizeof(T)) : kOobOffset;
+      const int off = (m < p.M && k < p.K) ? static_cast<int>(((int64_t)m * ldx + (k - kx)) * sizeof(T)) : kOobOffset;
       dma16(rX, off, 0, lds_addr(xl) + i * 1024);
     }
   }
@@ -467,12 +471,15 @@ int64_t skinny_split_workspace_bytes(int M, int N, int K) {
 // dot-product kernel below instead (comparison runs).
 bool skinny_split_eligible(const SkinnyArgs& a) {
   if (a.x_vec != 2 || a.M > 16) return false;
+  if (a.A2) return true;                      // [A | A2] exists only for the split kernel
   const char* v = std::getenv("GEV2_SKINNY_DOT");
   return !(v && v[0] == '1');
 }
 
 template <typename T>
 static hipError_t launch_skinny_t(const SkinnyArgs& a, float* part, hipStream_t s) {
+  if (a.A2 && (sizeof(T) != 2 || !skinny_split_eligible(a) || a.K1 <= 0 || a.K1 >= a.K || a.K1 % 256 != 0 || !part))
+    return hipErrorInvalidValue;
   if constexpr (sizeof(T) == 2) {
     // x_vec == 2: X rows are 16-byte aligned and span < 2^31 bytes (host)
     if (skinny_split_eligible(a)) return launch_skinny_split<T>(a, part, s);

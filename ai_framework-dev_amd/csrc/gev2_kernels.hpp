@@ -49,6 +49,13 @@ struct SkinnyArgs {
   int act, bias_kind;
   float slope, alpha;
   int x_vec;             // 1: X rows 16-byte aligned, K % chunk == 0; 2: also spans < 2^31 bytes
+  // Optional second part of X (split kernel only): columns K1 .. K-1 of X are
+  // columns 0 .. K-K1-1 of A2 (row stride lda2), so X = [A | A2] is never
+  // gathered.  K1 must be a multiple of 256 (a whole number of K blocks);
+  // A2 null: X is A alone.
+  const void* A2;
+  int64_t lda2;
+  int K1;
 };
 
 // Element-wise gZ = gY * act'(Z) (optionally scaled by beta) -> out, and

@@ -7,7 +7,10 @@
 // Forward, per step: one gather kernel writes XH = [X_t, h_{t-1}] ([N, I+H]),
 // then ONE operator forward XH . [Wx; Wh] (+ b, act) writes h_t and Z_t
 // straight into Y[:,t,:] and Z[:,t,:] through their row stride T*H, and the
-// next step reads h_t from Y.  The reference copies X_t and h_{t-1} in with
+// next step reads h_t from Y.  For 16-bit batches of at most 16 rows with I a
+// whole number of 256-row K blocks (and the operator scratch in the
+// descriptor), the skinny split-K kernel reads X_t and h_{t-1} in place
+// instead, and the gather launch goes.  The reference copies X_t and h_{t-1} in with
 // two 2-D copies and Y_rows / Z_rows out with two more per step.
 // Backward (BPTT), per step from T-1 down to 0: one gather kernel rebuilds
 // XH = [X_t, act(Z_{t-1}) or h0], forms G = dY_t + dh_next (dh_next = the
@@ -28,6 +31,7 @@
 
 #include "../../include/gev2_gemm.h"
 #include "gev2_device.hpp"
+#include "gev2_kernels.hpp"
 
 namespace gev2 {
 
@@ -200,6 +204,29 @@ int rnn_check(const D* d) {
   return GEV2_OK;
 }
 
+// 16-byte vector rows whose byte offsets from the base stay below 2^31 (the
+// split kernel's 32-bit buffer offsets).
+bool rows16(const void* p, int64_t ld, int64_t rows, int64_t cols, int64_t es) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld * es) % 16 == 0 && (cols * es) % 16 == 0 &&
+         ((rows - 1) * ld + cols) * es <= 0x7fffff00LL;
+}
+
+// The skinny split kernel reads XH = [X_t | h_{t-1}] from its two places, so
+// a step needs no gather launch, when: 16-bit data, N <= 16, I a whole number
+// of the kernel's 256-row K blocks, 16-byte rows of X, h0, Y and wcat within
+// 2^31 bytes, and the caller's 256-byte aligned workspace holds the partials.
+// Otherwise a step gathers XH and calls the operator.
+bool rnn_fwd_two_part(const gev2_rnn_desc* d) {
+  if (d->dtype == GEV2_F32 || d->N > gev2::kSkinnyMaxM || d->I % 256 != 0 || d->H % 8 != 0) return false;
+  if (std::getenv("GEV2_RNN_GATHER") || std::getenv("GEV2_NO_SKINNY")) return false;
+  const int64_t es = 2, T = d->T, IH = d->I + d->H;
+  if (!rows16(d->X, T * d->I, d->N, T * d->I, es) || !rows16(d->h0, d->H, d->N, d->H, es) ||
+      !rows16(d->Y, T * d->H, d->N, T * d->H, es) || !rows16(d->wcat, d->H, IH, d->H, es))
+    return false;
+  const int64_t need = gev2::skinny_split_workspace_bytes(d->N, d->H, static_cast<int>(IH));
+  return d->ws && (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0 && d->ws_bytes >= need;
+}
+
 int gemm_status(int st) {
   if (st != GEV2_OK) t_rnn_error = std::string("gemm: ") + gev2_last_error();
   return st;
@@ -327,8 +354,24 @@ int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
                                  (size_t)d->H * d->H * es, hipMemcpyDeviceToDevice, s), "pack Wh");
   if (st != GEV2_OK) return st;
   const int64_t ldy = (int64_t)d->T * d->H;
+  const bool two_part = rnn_fwd_two_part(d);
   for (int t = 0; t < d->T; ++t) {
     const void* hprev = t == 0 ? d->h0 : static_cast<const char*>(d->Y) + (size_t)(t - 1) * d->H * es;
+    if (two_part) {
+      gev2::SkinnyArgs a{};
+      a.A = static_cast<const char*>(d->X) + (size_t)t * d->I * es; a.lda = (int64_t)d->T * d->I;
+      a.A2 = hprev; a.lda2 = t == 0 ? d->H : ldy; a.K1 = d->I;
+      a.B = d->wcat; a.ldb = d->H;
+      a.D = static_cast<char*>(d->Y) + (size_t)t * d->H * es; a.ldd = ldy;
+      a.Zo = d->save_z ? static_cast<char*>(d->Z) + (size_t)t * d->H * es : nullptr; a.ldzo = ldy;
+      a.bias = d->bias; a.bias_kind = d->bias ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+      a.M = d->N; a.N = d->H; a.K = static_cast<int>(IH);
+      a.act = d->act; a.slope = d->leaky_slope; a.alpha = 1.f;
+      a.x_vec = 2;
+      st = hip_status(gev2::launch_skinny(d->dtype, a, static_cast<float*>(d->ws), s), "skinny step");
+      if (st != GEV2_OK) return st;
+      continue;
+    }
     st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_fwd_gather, d->X, hprev, t == 0 ? d->H : ldy, d->xh,
                                       dm, t, s), "gather");
     if (st != GEV2_OK) return st;

@@ -260,7 +260,12 @@ const char* gev2_conv2d_last_error(void);
  * [N,T,H], all contiguous, one dtype (F32 / F16 / BF16) except bias.
  * Workspaces (elements of dtype): xh N*(I+H), wcat (I+H)*H.  ws / ws_bytes:
  * optional scratch for the operator forward (gev2_gemm_fwd_desc.workspace).
- * One gather kernel and one operator forward per step.
+ * One gather kernel and one operator forward per step; with F16 / BF16, N <= 16,
+ * I a multiple of 256, H a multiple of 8, 16-byte aligned X, h0, Y and wcat,
+ * and ws holding the step's split-K partials (gev2_gemm_fwd_workspace_size of
+ * the step, 256-byte aligned), a step is instead the skinny split-K kernel
+ * reading X_t and h_{t-1} in place (no gather) plus its K-block sum, with the
+ * same results bit for bit (GEV2_RNN_GATHER=1 forces the gather form).
  * On a created (non-null) stream, when ws covers every step's operator scratch
  * (gev2_gemm_fwd_workspace_size / gev2_gemm_bwd_workspace_size of one step),
  * the step loop of a descriptor seen before is recorded into a HIP graph on

@@ -221,3 +221,71 @@ def test_rnn_graph_replays(env, dtype):
                 assert np.array_equal(got[k], ref[k]), (call, k)
     finally:
         stream.destroy()
+
+
+@pytest.mark.parametrize("shape", [(8, 4, 512, 1024), (13, 3, 256, 264), (1, 2, 768, 128)],
+                         ids=["N8-I512-H1024", "N13-H264", "N1-K896"])
+def test_rnn_fwd_two_part_matches_gather(gpu, monkeypatch, shape):
+    """16-bit, N <= 16, I a multiple of 256, with the operator scratch in the descriptor: each
+    forward step is the skinny split kernel reading X_t and h_{t-1} where they lie, with no
+    gather launch.  Its Y and Z equal, bit for bit, those of the gather + operator path
+    (GEV2_RNN_GATHER=1: same kernel over the gathered rows, same K order), and each step is
+    within a few bf16 roundings of the float64 step fed the device's own h_{t-1}.  Shapes:
+    the benchmark's step; 13 rows and 264 columns (a ragged column slab); K = 896 (the last
+    K block half empty)."""
+    import ctypes
+    from graph_executor_v2.ops import capi
+    N, T, I, H = shape
+    dtype = BF16
+    es = capi.elem_bytes(dtype)
+    L = capi.lib()
+    X, Wx, Wh, h0, b, _ = _inputs(41, N, T, I, H)
+    X, Wx, Wh, h0 = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0))
+    IH = I + H
+    bufs = []
+
+    def buf(nbytes):
+        d = capi.DeviceBuffer(max(nbytes, 16))
+        bufs.append(d)
+        return d.ptr
+
+    def put(a):
+        d = capi.DeviceBuffer.from_numpy(capi.to_storage(a, dtype))
+        bufs.append(d)
+        return d.ptr
+
+    try:
+        gX, gWx, gWh, gh0 = (put(a) for a in (X, Wx, Wh, h0))
+        gb = capi.DeviceBuffer.from_numpy(b)
+        bufs.append(gb)
+        st = capi.to_storage(np.zeros(1, np.float32), dtype).dtype
+        outs = []
+        for gather in ("0", "1"):
+            if gather == "1":
+                monkeypatch.setenv("GEV2_RNN_GATHER", "1")
+            Y, Z = buf(N * T * H * es), buf(N * T * H * es)
+            ws_bytes = 4 << 20
+            fd = capi.RnnDesc(dtype=dtype, act=capi.ACT["tanh"], save_z=1, N=N, T=T, I=I, H=H, X=gX, Wx=gWx,
+                              Wh=gWh, bias=gb.ptr, h0=gh0, Y=Y, Z=Z, xh=buf(N * IH * es), wcat=buf(IH * H * es),
+                              ws=buf(ws_bytes), ws_bytes=ws_bytes)
+            capi.check_rnn(L.gev2_rnn_fwd(ctypes.byref(fd), None), f"fwd gather={gather}")
+            capi.synchronize()
+            got = {}
+            for k, p in (("Y", Y), ("Z", Z)):
+                a = np.empty((N, T, H), st)
+                capi.check(L.gev2_memcpy_dtoh(a.ctypes.data, p, a.nbytes), "dtoh")
+                got[k] = capi.from_storage(a, dtype).astype(np.float64)
+            outs.append(got)
+        monkeypatch.delenv("GEV2_RNN_GATHER")
+    finally:
+        for d in bufs:
+            d.free()
+    assert np.array_equal(outs[0]["Z"], outs[1]["Z"])
+    assert np.array_equal(outs[0]["Y"], outs[1]["Y"])
+    Z, Yd = outs[0]["Z"], outs[0]["Y"]
+    eps = 2.0 ** -8
+    for t in range(T):
+        hprev = h0 if t == 0 else Yd[:, t - 1]
+        zt = X[:, t] @ Wx + hprev @ Wh + b
+        mag = np.abs(X[:, t]) @ np.abs(Wx) + np.abs(hprev) @ np.abs(Wh) + np.abs(b)
+        assert np.all(np.abs(Z[:, t] - zt) <= 2 * eps * mag + 1e-6), t
