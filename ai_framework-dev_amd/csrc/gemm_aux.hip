@@ -260,22 +260,41 @@ __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
   float acc[16];
 #pragma unroll
   for (int m = 0; m < 16; ++m) acc[m] = 0.f;
-  for (int n0 = lane * EPC; n0 < p.N; n0 += 64 * EPC) {
-    float bv[EPC];
-    chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(brow + n0), bv);
+  // two passes of 64 chunks at a time, so that both passes' loads are in
+  // flight together; a second pass past N reloads the first and adds nothing
+  for (int n0 = lane * EPC; n0 < p.N; n0 += 128 * EPC) {
+    const int n1 = n0 + 64 * EPC;
+    const bool two = n1 < p.N;
+    const int nb = two ? n1 : n0;
+    u32x4 braw[2], graw[2][16];
+    braw[0] = *reinterpret_cast<const u32x4*>(brow + n0);
+    braw[1] = *reinterpret_cast<const u32x4*>(brow + nb);
 #pragma unroll
     for (int m = 0; m < 16; ++m) {
       if (m >= p.M) continue;
-      float gv[EPC];
-      chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0), gv);
-      if (Z) {
-        float zv[EPC];
-        chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n0), zv);
+      graw[0][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0);
+      graw[1][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + nb);
+    }
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) gv[e] *= act_grad(zv[e], p.act, p.slope);
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && !two) break;
+      const int n = h == 0 ? n0 : nb;
+      float bv[EPC];
+      chunk_to_f32<T>(braw[h], bv);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        if (m >= p.M) continue;
+        float gv[EPC];
+        chunk_to_f32<T>(graw[h][m], gv);
+        if (Z) {
+          float zv[EPC];
+          chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n), zv);
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) gv[e] *= act_grad(zv[e], p.act, p.slope);
+        }
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[m] = fmaf(gv[e], bv[e], acc[m]);
       }
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) acc[m] = fmaf(gv[e], bv[e], acc[m]);
     }
   }
   T* D = reinterpret_cast<T*>(p.D);
