@@ -19,6 +19,10 @@
 // dXH = G' [Wx; Wh]^T, dWcat_t = XH^T G' and dB_t; one kernel adds dWcat_t
 // and dB_t to fp32 sums in step order.  dB is the sum over all steps (the
 // reference's per-step GEMM backward zero-fills it, so it keeps step 0's only).
+// With N <= 16 and N*T <= I+H (rnn_bwd_gathered) the step is shorter: the
+// gather kernel writes G'_t = G * act'(Z_t) into an [N, T, H] buffer and the
+// step runs only dXH = G'_t Wcat^T; dWx = X^T G', dWh = Hprev^T G' and dB are
+// formed once after the loop, each a sum of depth N*T rounded once.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -79,6 +83,58 @@ __global__ void __launch_bounds__(256) rnn_bwd_gather_kernel(const T* __restrict
     if (!last) gy += Elem<T>::load1(dxh + idx);
     Elem<T>::store1(g + (int64_t)n * d.H + h, gy);
   }
+}
+
+// Step t of the backward in the gathered-G' form (N <= 16):
+//   G'[n, t, :] = (dY[n, t, :] + (t < T-1 ? dxh[n, I:] : 0)) * act'(Z[n, t, :])
+//   dX[n, t+1, :] = dxh[n, :I]            (t < T-1, dX requested)
+// G' ([N, T, H], row stride T*H) is kept for the weight gradients after the loop.
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_bwd_gather_g_kernel(const T* __restrict__ Z, const T* __restrict__ dY,
+                                                               const T* __restrict__ dxh, T* __restrict__ gall,
+                                                               T* __restrict__ dX, RnnDims d, int t, int act,
+                                                               float slope) {
+  const int IH = d.I + d.H;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)d.N * IH) return;
+  const int n = static_cast<int>(idx / IH), j = static_cast<int>(idx - (int64_t)n * IH);
+  const bool last = t == d.T - 1;
+  if (j < d.I) {
+    if (dX && !last) dX[((int64_t)n * d.T + t + 1) * d.I + j] = dxh[idx];
+  } else {
+    const int h = j - d.I;
+    const int64_t o = ((int64_t)n * d.T + t) * d.H + h;
+    float gy = Elem<T>::load1(dY + o);
+    if (!last) gy += Elem<T>::load1(dxh + idx);
+    Elem<T>::store1(gall + o, gy * act_grad(Elem<T>::load1(Z + o), act, slope));
+  }
+}
+
+// hprev[n, t, :] = t > 0 ? act(Z[n, t-1, :]) : h0[n, :]   ([N, T, H])
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_hprev_kernel(const T* __restrict__ Z, const T* __restrict__ h0,
+                                                        T* __restrict__ hprev, RnnDims d, int act, float slope) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)d.N * d.T * d.H) return;
+  const int h = static_cast<int>(idx % d.H);
+  const int64_t nt = idx / d.H;
+  const int t = static_cast<int>(nt % d.T), n = static_cast<int>(nt / d.T);
+  if (t > 0)
+    Elem<T>::store1(hprev + idx, act_fwd(Elem<T>::load1(Z + idx - d.H), act, slope));
+  else
+    hprev[idx] = h0[(int64_t)n * d.H + h];
+}
+
+// dB[h] = sum over the rows r = 0 .. rows-1 of g[r, h], in row order (fp32).
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_colsum_kernel(const T* __restrict__ g, int64_t rows, int H,
+                                                         float* __restrict__ dB) {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float s = 0.f;
+#pragma unroll 8
+  for (int64_t r = 0; r < rows; ++r) s += Elem<T>::load1(g + r * H + h);
+  dB[h] = s;
 }
 
 // dwcat[i] = (first ? 0 : dwcat[i]) + tmpw[i];  dB[h] likewise from gb
@@ -185,6 +241,30 @@ hipError_t launch_acc(float* dwcat, const void* tmpw, int64_t nw, float* dB, con
 }
 
 template <typename T>
+hipError_t launch_bwd_gather_g(const void* Z, const void* dY, const void* dxh, void* gall, void* dX,
+                               const RnnDims& d, int t, int act, float slope, hipStream_t s) {
+  hipLaunchKernelGGL((rnn_bwd_gather_g_kernel<T>), dim3(blocks_for((int64_t)d.N * (d.I + d.H))), dim3(256), 0, s,
+                     static_cast<const T*>(Z), static_cast<const T*>(dY), static_cast<const T*>(dxh),
+                     static_cast<T*>(gall), static_cast<T*>(dX), d, t, act, slope);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_hprev(const void* Z, const void* h0, void* hprev, const RnnDims& d, int act, float slope,
+                        hipStream_t s) {
+  hipLaunchKernelGGL((rnn_hprev_kernel<T>), dim3(blocks_for((int64_t)d.N * d.T * d.H)), dim3(256), 0, s,
+                     static_cast<const T*>(Z), static_cast<const T*>(h0), static_cast<T*>(hprev), d, act, slope);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_colsum(const void* g, int64_t rows, int H, float* dB, hipStream_t s) {
+  hipLaunchKernelGGL((rnn_colsum_kernel<T>), dim3((H + 255) / 256), dim3(256), 0, s, static_cast<const T*>(g),
+                     rows, H, dB);
+  return hipGetLastError();
+}
+
+template <typename T>
 hipError_t launch_bwd_finish(const void* dxh, const float* dwcat, void* dX, void* dh0, void* dWx, void* dWh,
                              const RnnDims& d, hipStream_t s) {
   const int64_t n = (int64_t)d.N * (d.I + d.H) + (int64_t)(d.I + d.H) * d.H;
@@ -253,6 +333,33 @@ bool rnn_fwd_two_part(const gev2_rnn_desc* d) {
     return false;
   const int64_t need = gev2::skinny_split_workspace_bytes(d->N, d->H, static_cast<int>(IH));
   return d->ws && (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0 && d->ws_bytes >= need;
+}
+
+// The backward's gathered-G' form: each step forms G'_t straight into an
+// [N, T, H] buffer (tmpw) and runs only dXH = G'_t Wcat^T (skinny NT kernel);
+// after the loop dWx = X^T G' and dWh = Hprev^T G' are one operator forward
+// each (depth N*T, one rounding), Hprev staged in dwcat, and dB is a column
+// sum of G'.  Needs N <= 16, 16-byte rows of G' and wcat, and N*T <= I+H (so
+// that G' fits tmpw and Hprev fits dwcat).  GEV2_RNN_STEP_DW=1 keeps the
+// per-step form (one operator backward and one accumulation per step).
+bool rnn_bwd_gathered(const gev2_rnn_bwd_desc* d) {
+  const int64_t es = esize(d->dtype);
+  if (d->N > gev2::kSkinnyMaxM || (int64_t)d->N * d->T > (int64_t)d->I + d->H || (d->H * es) % 16 != 0) return false;
+  if (std::getenv("GEV2_RNN_STEP_DW")) return false;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return al(d->tmpw) && al(d->wcat) && al(d->dwcat);
+}
+
+// dW = A^T G' over the N*T rows (A: X or the staged Hprev), as an operator forward
+gev2_gemm_fwd_desc rnn_wgrad_desc(const gev2_rnn_bwd_desc* d, const void* A, int64_t lda, int M, void* out) {
+  gev2_gemm_fwd_desc f{};
+  f.dtype = d->dtype; f.act = GEV2_ACT_NONE; f.alpha = 1.f; f.bias_kind = GEV2_BIAS_NONE;
+  f.M = M; f.N = d->H; f.K = (int64_t)d->N * d->T; f.batch = 1;
+  f.A = A; f.lda = lda; f.trans_a = 1;
+  f.B = d->tmpw; f.ldb = d->H;
+  f.Y = out; f.ldy = d->H;
+  f.workspace = d->ws; f.workspace_bytes = d->ws_bytes;
+  return f;
 }
 
 int gemm_status(int st) {
@@ -440,7 +547,16 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
     return st;
   }
   bool graph_ok;
-  {
+  if (rnn_bwd_gathered(d)) {
+    // the weight-gradient GEMMs must run with the descriptor's scratch (or none)
+    // when recorded, as they do eagerly
+    auto fits = [&](const gev2_gemm_fwd_desc& f) {
+      if (!f.Y) return true;                     // that gradient is not requested
+      const int64_t need = gev2_gemm_fwd_workspace_size(&f);
+      return need == 0 || (need > 0 && d->ws && d->ws_bytes >= need && (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0);
+    };
+    graph_ok = fits(rnn_wgrad_desc(d, d->X, d->I, d->I, d->dWx)) && fits(rnn_wgrad_desc(d, d->dwcat, d->H, d->H, d->dWh));
+  } else {
     gev2_gemm_bwd_desc b{};
     b.dtype = d->dtype; b.act = d->act; b.alpha = 1.f; b.bias_kind = d->dB ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
     b.M = d->N; b.N = d->H; b.K = IH; b.batch = 1;
@@ -463,6 +579,43 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
   if (st != GEV2_OK) return st;
   const int64_t ldz = (int64_t)d->T * d->H;
   const bool want_w = d->dWx || d->dWh;
+  if (rnn_bwd_gathered(d)) {
+    for (int t = d->T - 1; t >= 0; --t) {
+      st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_gather_g, d->Z, d->dY, d->dxh, d->tmpw, d->dX,
+                                        dm, t, d->act, d->leaky_slope, s), "gather G'");
+      if (st != GEV2_OK) return st;
+      gev2::SkinnyNtArgs a{};
+      a.G = static_cast<const char*>(d->tmpw) + (size_t)t * d->H * es; a.ldg = ldz;
+      a.Z = nullptr; a.ldz = 0;
+      a.B = d->wcat; a.ldb = d->H;
+      a.D = d->dxh; a.ldd = IH;
+      a.M = d->N; a.N = d->H; a.K = static_cast<int>(IH);
+      a.act = GEV2_ACT_NONE; a.slope = 0.f; a.alpha = 1.f;
+      st = hip_status(gev2::launch_skinny_nt(d->dtype, a, s), "dXH");
+      if (st != GEV2_OK) return st;
+    }
+    const int64_t rows = (int64_t)d->N * d->T;
+    auto wgrad = [&](const void* A, int64_t lda, int M, void* out) -> int {
+      const gev2_gemm_fwd_desc f = rnn_wgrad_desc(d, A, lda, M, out);
+      return gemm_status(gev2_gemm_fwd(&f, stream));
+    };
+    if (d->dWx) {
+      st = wgrad(d->X, d->I, d->I, d->dWx);
+      if (st != GEV2_OK) return st;
+    }
+    if (d->dWh) {
+      st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_hprev, d->Z, d->h0, d->dwcat, dm, d->act,
+                                        d->leaky_slope, s), "hprev");
+      if (st == GEV2_OK) st = wgrad(d->dwcat, d->H, d->H, d->dWh);
+      if (st != GEV2_OK) return st;
+    }
+    if (d->dB) {
+      st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_colsum, d->tmpw, rows, d->H, d->dB, s), "dB");
+      if (st != GEV2_OK) return st;
+    }
+    return hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_finish, d->dxh, d->dwcat, d->dX, d->dh0,
+                                        nullptr, nullptr, dm, s), "finish");
+  }
   for (int t = d->T - 1; t >= 0; --t) {
     st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_gather, d->X, d->Z, d->h0, d->dY, d->dxh, d->xh,
                                       d->g, d->dX, dm, t, d->act, d->leaky_slope, s), "gather");

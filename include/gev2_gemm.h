@@ -296,6 +296,12 @@ typedef struct gev2_rnn_desc {
  * (elements of dtype unless noted): xh N*(I+H), g N*H, wcat (I+H)*H,
  * dxh N*(I+H), tmpw (I+H)*H, dwcat (I+H)*H floats, gb H floats.  ws / ws_bytes:
  * optional dY' scratch of the operator backward (gev2_gemm_bwd_desc.workspace).
+ * With N <= 16, N*T <= I+H, H*elem a multiple of 16 bytes and 16-byte aligned
+ * tmpw, wcat and dwcat, a step is one gather kernel (G' = (dY_t + dh_next) *
+ * act'(Z_t) kept for all steps in tmpw as [N,T,H]) and one dXH product; dWx =
+ * X^T G', dWh = Hprev^T G' (Hprev staged in dwcat) and dB are formed after the
+ * loop (GEV2_RNN_STEP_DW=1 keeps one operator backward per step).  ws then
+ * serves those two weight-gradient products.
  */
 typedef struct gev2_rnn_bwd_desc {
   int32_t dtype;

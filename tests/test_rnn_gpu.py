@@ -103,6 +103,53 @@ def test_rnn_exact_integers(env):
         assert np.array_equal(out[k], ref[k]), k
 
 
+@pytest.mark.parametrize("form", ["gathered", "per-step"])
+def test_rnn_exact_integers_both_backward_forms(env, monkeypatch, form):
+    """H = 8 (32-byte fp32 rows) and N*T <= I+H: the backward forms G' into one [N, T, H]
+    buffer and computes dWx, dWh (one GEMM of depth N*T each) and dB after the loop;
+    GEV2_RNN_STEP_DW=1 keeps one operator backward and one accumulation per step.  Integer
+    inputs keep every sum exact, so both forms must equal the oracle bit for bit."""
+    if form == "per-step":
+        monkeypatch.setenv("GEV2_RNN_STEP_DW", "1")
+    r = np.random.default_rng(18)
+    N, T, I, H = 3, 4, 8, 8
+    X = r.integers(-2, 3, (N, T, I)).astype(np.float32)
+    Wx, Wh = (r.integers(-1, 2, s).astype(np.float32) for s in ((I, H), (H, H)))
+    h0 = r.integers(-2, 3, (N, H)).astype(np.float32)
+    b = r.integers(-3, 4, H).astype(np.float32)
+    dY = r.integers(-2, 3, (N, T, H)).astype(np.float32)
+    out = _run(env, X, Wx, Wh, h0, b, "relu", dY=dY)
+    Y64, Z64 = O.rnn_forward(X, Wx, Wh, h0, b, "relu")
+    assert np.array_equal(out["Z"], Z64) and np.array_equal(out["Y"], Y64)
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, Z64, "relu")
+    for k in ("dWx", "dWh", "dB", "dh0", "dX"):
+        assert np.array_equal(out[k], ref[k]), k
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_rnn_backward_forms_agree(env, monkeypatch, dtype):
+    """The gathered-G' backward against the per-step one on the benchmark's shape class
+    (N 8, I 512, H 1024, fewer steps): dh0 and dX are the same chain of dXH products (equal
+    up to the per-step form's rounding of G before act'), dWx / dWh / dB differ only in
+    summation order and rounding (one rounding of a depth-N*T sum against T roundings)."""
+    N, T, I, H = 8, 4, 512, 1024
+    X, Wx, Wh, h0, b, dY = _inputs(19, N, T, I, H)
+    if dtype == BF16:
+        X, Wx, Wh, h0, dY = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0, dY))
+    outs = []
+    for form in ("gathered", "per-step"):
+        if form == "per-step":
+            monkeypatch.setenv("GEV2_RNN_STEP_DW", "1")
+        outs.append(_run(env, X, Wx, Wh, h0, b, "tanh", dY=dY, dtype=dtype))
+    assert np.array_equal(outs[0]["Z"], outs[1]["Z"])
+    ref = O.rnn_backward(X, Wx, Wh, h0, dY, outs[0]["Z"].astype(np.float64), "tanh")
+    tol = 1e-4 if dtype == F32 else 0.05
+    for k in ("dWx", "dWh", "dB", "dh0", "dX"):
+        for o in outs:
+            rel = np.abs(o[k].astype(np.float64) - ref[k]).max() / max(1e-6, np.abs(ref[k]).max())
+            assert rel <= tol, (k, rel)
+
+
 def test_rnn_subset_of_gradients(env):
     """Only dWh and dB requested: the others stay untouched, the requested ones are unchanged."""
     N, T, I, H = 5, 3, 8, 16
