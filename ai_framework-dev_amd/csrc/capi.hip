@@ -274,7 +274,6 @@ struct FwdPlan {
 // tiles, a reduction of 128-2048 and 2^26 multiply-adds, where the tile
 // kernels would run as a handful of workgroups (or split K over a second
 // pass).  GEV2_NO_SMALL=1 turns it off.
-int small_waves_for(int64_t red) { return red >= 512 ? 16 : 4; }
 
 // a small-kernel operand, with its 16-byte-load flag
 gev2::SmallOperand small_op(const void* p, int64_t rs, int64_t ks, const void* z = nullptr, int64_t zrs = 0,
@@ -289,7 +288,7 @@ void plan_small(const gev2_gemm_fwd_desc* d, FwdPlan* pl) {
   if (d->dtype != GEV2_F32 || d->batch != 1 || env_int("GEV2_NO_SMALL", 0) != 0) return;
   const int64_t tiles = ((M + 15) / 16) * ((N + 15) / 16);
   if (tiles > 512 || K < 128 || K > 2048 || static_cast<double>(M) * N * K > 67108864.0) return;
-  pl->small_waves = small_waves_for(K);
+  pl->small_waves = gev2::small_waves_for(K);
 }
 
 // Slices of a split reduction of depth R over `tiles` output tiles: enough
@@ -626,7 +625,7 @@ int small_bwd_waves(const gev2_gemm_bwd_desc* d) {
   int64_t split_red = 0;
   if (d->gA && N > kSmallOwnRed) split_red = std::max(split_red, N);
   if (d->gB && M > kSmallOwnRed) split_red = std::max(split_red, M);
-  const int w = small_waves_for(split_red);
+  const int w = gev2::small_waves_for(split_red);
   // at most 2048 output tiles in all: past that (the rank-8 dW of an RNN step,
   // 6144 tiles) one launch measured no faster than the multi-launch path
   const int64_t tiles = (d->gA ? ((M + 15) / 16) * ((K + 15) / 16) : 0) +

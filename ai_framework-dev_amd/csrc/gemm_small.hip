@@ -32,12 +32,17 @@ namespace gev2 {
 // times act'(Z) when it is dY' (HASZ).  VEC operands (k contiguous, rows and
 // base 16-byte aligned) take one 16-byte load per array when all four are in
 // range.
-template <bool VEC, bool HASZ, int ACT>
+template <bool VEC, bool HASZ, int ACT, bool TWO = false>
 __device__ __forceinline__ f32x4_t small_load4(const SmallOperand& o, int i, int k0, int red, float slope) {
   f32x4_t v;
+  // TWO: the part holding k0 .. k0+3 (k0 and k1 are multiples of 4, so the
+  // four never straddle k1); element k of it is pb[ob + k * ks]
+  const bool second = TWO && k0 >= o.k1;
+  const float* pb = second ? o.p2 : o.p;
+  const int64_t ob = second ? (int64_t)i * o.rs2 - (int64_t)o.k1 * o.ks : (int64_t)i * o.rs;
   if constexpr (VEC) {
     if (k0 + 3 < red) {
-      v = *reinterpret_cast<const f32x4_t*>(o.p + (int64_t)i * o.rs + k0);
+      v = *reinterpret_cast<const f32x4_t*>(pb + (ob + k0));
       if constexpr (HASZ) {
         const f32x4_t z = *reinterpret_cast<const f32x4_t*>(o.z + (int64_t)i * o.zrs + k0);
 #pragma unroll
@@ -51,7 +56,7 @@ __device__ __forceinline__ f32x4_t small_load4(const SmallOperand& o, int i, int
     const int k = k0 + e;
     float x = 0.f;
     if (k < red) {
-      x = o.p[(int64_t)i * o.rs + (int64_t)k * o.ks];
+      x = pb[ob + (int64_t)k * o.ks];
       if constexpr (HASZ) x *= act_grad_t<ACT>(o.z[(int64_t)i * o.zrs + (int64_t)k * o.zks], slope);
     }
     v[e] = x;
@@ -60,7 +65,7 @@ __device__ __forceinline__ f32x4_t small_load4(const SmallOperand& o, int i, int
 }
 
 // One 16x16 output tile t of job J; red: W x 256 floats of LDS.
-template <int W, bool AV, bool BV, bool AZ, bool BZ, int ACT, bool FWD>
+template <int W, bool AV, bool BV, bool AZ, bool BZ, int ACT, bool FWD, bool TWO = false>
 __device__ __forceinline__ void small_tile(const SmallArgs& p, const SmallJob& J, int t, float* red) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -77,7 +82,7 @@ __device__ __forceinline__ void small_tile(const SmallArgs& p, const SmallJob& J
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int k0 = 16 * (j0 + u * W) + 4 * kq;
-      av[u] = rin ? small_load4<AV, AZ, ACT>(J.a, r, k0, J.red, p.slope) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      av[u] = rin ? small_load4<AV, AZ, ACT, TWO>(J.a, r, k0, J.red, p.slope) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       bv[u] = cin ? small_load4<BV, BZ, ACT>(J.b, c, k0, J.red, p.slope) : f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
@@ -176,10 +181,11 @@ __device__ __forceinline__ void small_dbias(const SmallArgs& p, int b, float* pa
 }
 
 // Forward: job 0, A / B contiguous along K (AV / BV) or not.
-template <int W, bool AV, bool BV>
+// TWO: the X operand comes in two parts (SmallOperand::p2)
+template <int W, bool AV, bool BV, bool TWO = false>
 __global__ void __launch_bounds__(W * 64) small_fwd_kernel(SmallArgs p) {
   __shared__ float red[W * 256];
-  small_tile<W, AV, BV, false, false, kActNone, true>(p, p.job[0], blockIdx.x, red);
+  small_tile<W, AV, BV, false, false, kActNone, true, TWO>(p, p.job[0], blockIdx.x, red);
 }
 
 // Backward: tiles of the jobs (kind 1: dX, dY' on the left; kind 2: dW, dY'
@@ -211,7 +217,12 @@ template <int W>
 static hipError_t launch_small_w(const SmallArgs& a, int wgs, hipStream_t s) {
   if (a.fwd) {
     const bool av = a.job[0].a.vec, bv = a.job[0].b.vec;
-    if (av && bv) hipLaunchKernelGGL((small_fwd_kernel<W, true, true>), dim3(wgs), dim3(W * 64), 0, s, a);
+    if (a.job[0].a.p2) {
+      if (av && bv) hipLaunchKernelGGL((small_fwd_kernel<W, true, true, true>), dim3(wgs), dim3(W * 64), 0, s, a);
+      else if (av) hipLaunchKernelGGL((small_fwd_kernel<W, true, false, true>), dim3(wgs), dim3(W * 64), 0, s, a);
+      else if (bv) hipLaunchKernelGGL((small_fwd_kernel<W, false, true, true>), dim3(wgs), dim3(W * 64), 0, s, a);
+      else hipLaunchKernelGGL((small_fwd_kernel<W, false, false, true>), dim3(wgs), dim3(W * 64), 0, s, a);
+    } else if (av && bv) hipLaunchKernelGGL((small_fwd_kernel<W, true, true>), dim3(wgs), dim3(W * 64), 0, s, a);
     else if (av) hipLaunchKernelGGL((small_fwd_kernel<W, true, false>), dim3(wgs), dim3(W * 64), 0, s, a);
     else if (bv) hipLaunchKernelGGL((small_fwd_kernel<W, false, true>), dim3(wgs), dim3(W * 64), 0, s, a);
     else hipLaunchKernelGGL((small_fwd_kernel<W, false, false>), dim3(wgs), dim3(W * 64), 0, s, a);
@@ -234,6 +245,8 @@ static hipError_t launch_small_w(const SmallArgs& a, int wgs, hipStream_t s) {
   }
   return hipGetLastError();
 }
+
+int small_waves_for(int64_t red) { return red >= 512 ? 16 : 4; }
 
 hipError_t launch_small(const SmallArgs& a, int waves, hipStream_t s) {
   int wgs = 0;

@@ -121,6 +121,9 @@ struct SmallOperand {
   const float* p; int64_t rs, ks;
   const float* z; int64_t zrs, zks;
   int vec;
+  // Optional second part (no z with it): reduction indices k1 .. of rows i are
+  // p2[i * rs2 + (k - k1) * ks]; k1 a multiple of 4.  p2 null: p alone.
+  const float* p2; int64_t rs2; int k1;
 };
 // out[rows, cols] (leading dimension ldo) = scale * sum_k a(row, k) b(col, k);
 // kind 0: forward, 1: dX (a is dY'), 2: dW (b is dY').  own (backward only):
@@ -152,6 +155,8 @@ struct SmallArgs {
 };
 // waves per workgroup: 4 or 16
 hipError_t launch_small(const SmallArgs& a, int waves, hipStream_t s);
+// waves per workgroup for a reduction of length red: 16 from 512 on, else 4
+int small_waves_for(int64_t red);
 hipError_t launch_finish_col_sums(const float* partial, int64_t sPartial, int row_blocks, int N,
                                   float* gbias, int64_t sGbias, int batch, hipStream_t s);
 

@@ -362,6 +362,17 @@ gev2_gemm_fwd_desc rnn_wgrad_desc(const gev2_rnn_bwd_desc* d, const void* A, int
   return f;
 }
 
+// fp32: the one-launch small kernel takes XH = [X_t | h_{t-1}] as a two-part
+// operand (no gather) within its limits (at most 512 16x16 output tiles, a
+// reduction I+H of 128-2048, 2^26 multiply-adds) and with I a multiple of 4.
+bool rnn_fwd_small_two_part(const gev2_rnn_desc* d) {
+  const int64_t IH = (int64_t)d->I + d->H;
+  if (d->dtype != GEV2_F32 || d->I % 4 != 0 || std::getenv("GEV2_RNN_GATHER") || std::getenv("GEV2_NO_SMALL"))
+    return false;
+  const int64_t tiles = ((int64_t)(d->N + 15) / 16) * ((d->H + 15) / 16);
+  return tiles <= 512 && IH >= 128 && IH <= 2048 && static_cast<double>(d->N) * d->H * IH <= 67108864.0;
+}
+
 int gemm_status(int st) {
   if (st != GEV2_OK) t_rnn_error = std::string("gemm: ") + gev2_last_error();
   return st;
@@ -490,8 +501,35 @@ int gev2_rnn_fwd(const gev2_rnn_desc* d, void* stream) {
   if (st != GEV2_OK) return st;
   const int64_t ldy = (int64_t)d->T * d->H;
   const bool two_part = rnn_fwd_two_part(d);
+  const bool small_two_part = rnn_fwd_small_two_part(d);
   for (int t = 0; t < d->T; ++t) {
     const void* hprev = t == 0 ? d->h0 : static_cast<const char*>(d->Y) + (size_t)(t - 1) * d->H * es;
+    if (small_two_part) {
+      gev2::SmallArgs a{};
+      gev2::SmallJob& J = a.job[0];
+      const float* xt = static_cast<const float*>(d->X) + (size_t)t * d->I;
+      const float* hp = static_cast<const float*>(hprev);
+      const int64_t ldh = t == 0 ? d->H : ldy;
+      J.a.p = xt; J.a.rs = (int64_t)d->T * d->I; J.a.ks = 1;
+      J.a.p2 = hp; J.a.rs2 = ldh; J.a.k1 = d->I;
+      J.a.vec = J.a.rs % 4 == 0 && ldh % 4 == 0 && (reinterpret_cast<uintptr_t>(xt) & 15) == 0 &&
+                (reinterpret_cast<uintptr_t>(hp) & 15) == 0;
+      J.b.p = static_cast<const float*>(d->wcat); J.b.rs = 1; J.b.ks = d->H;
+      J.kind = 0;
+      J.rows = d->N; J.cols = d->H; J.red = static_cast<int>(IH);
+      J.tiles_c = (d->H + 15) / 16;
+      J.tiles = ((d->N + 15) / 16) * J.tiles_c;
+      J.wgs = J.tiles;
+      J.scale = 1.f;
+      J.out = static_cast<float*>(d->Y) + (size_t)t * d->H; J.ldo = ldy;
+      a.njobs = 1; a.fwd = 1;
+      a.act = d->act; a.slope = d->leaky_slope;
+      a.bias = d->bias; a.bias_kind = d->bias ? GEV2_BIAS_PER_N : GEV2_BIAS_NONE;
+      a.Z = d->save_z ? static_cast<float*>(d->Z) + (size_t)t * d->H : nullptr; a.ldz = ldy;
+      st = hip_status(gev2::launch_small(a, gev2::small_waves_for(IH), s), "small step");
+      if (st != GEV2_OK) return st;
+      continue;
+    }
     if (two_part) {
       gev2::SkinnyArgs a{};
       a.A = static_cast<const char*>(d->X) + (size_t)t * d->I * es; a.lda = (int64_t)d->T * d->I;

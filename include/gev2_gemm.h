@@ -265,7 +265,10 @@ const char* gev2_conv2d_last_error(void);
  * and ws holding the step's split-K partials (gev2_gemm_fwd_workspace_size of
  * the step, 256-byte aligned), a step is instead the skinny split-K kernel
  * reading X_t and h_{t-1} in place (no gather) plus its K-block sum, with the
- * same results bit for bit (GEV2_RNN_GATHER=1 forces the gather form).
+ * same results bit for bit (GEV2_RNN_GATHER=1 forces the gather form).  F32
+ * steps within the one-launch small kernel's limits (I+H in 128..2048, at
+ * most 512 16x16 output tiles, I a multiple of 4) read X_t and h_{t-1} in
+ * place too, with or without ws.
  * On a created (non-null) stream, when ws covers every step's operator scratch
  * (gev2_gemm_fwd_workspace_size / gev2_gemm_bwd_workspace_size of one step),
  * the step loop of a descriptor seen before is recorded into a HIP graph on

@@ -270,24 +270,25 @@ def test_rnn_graph_replays(env, dtype):
         stream.destroy()
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("shape", [(8, 4, 512, 1024), (13, 3, 256, 264), (1, 2, 768, 128)],
                          ids=["N8-I512-H1024", "N13-H264", "N1-K896"])
-def test_rnn_fwd_two_part_matches_gather(gpu, monkeypatch, shape):
-    """16-bit, N <= 16, I a multiple of 256, with the operator scratch in the descriptor: each
-    forward step is the skinny split kernel reading X_t and h_{t-1} where they lie, with no
-    gather launch.  Its Y and Z equal, bit for bit, those of the gather + operator path
-    (GEV2_RNN_GATHER=1: same kernel over the gathered rows, same K order), and each step is
-    within a few bf16 roundings of the float64 step fed the device's own h_{t-1}.  Shapes:
-    the benchmark's step; 13 rows and 264 columns (a ragged column slab); K = 896 (the last
-    K block half empty)."""
+def test_rnn_fwd_two_part_matches_gather(gpu, monkeypatch, shape, dtype):
+    """The forward step reads X_t and h_{t-1} where they lie, with no gather launch: 16-bit
+    (N <= 16, I a multiple of 256, operator scratch in the descriptor) through the skinny
+    split kernel, fp32 through the one-launch small kernel.  Its Y and Z equal, bit for bit,
+    those of the gather + operator path (GEV2_RNN_GATHER=1: the same kernel over the gathered
+    rows, same reduction order), and each step is within the storage type's roundings of the
+    float64 step fed the device's own h_{t-1}.  Shapes: the benchmark's step; 13 rows and 264
+    columns (a ragged column slab / tile); K = 896 (the last 256-row K block half empty)."""
     import ctypes
     from graph_executor_v2.ops import capi
     N, T, I, H = shape
-    dtype = BF16
     es = capi.elem_bytes(dtype)
     L = capi.lib()
     X, Wx, Wh, h0, b, _ = _inputs(41, N, T, I, H)
-    X, Wx, Wh, h0 = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0))
+    if dtype == BF16:
+        X, Wx, Wh, h0 = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0))
     IH = I + H
     bufs = []
 
@@ -330,9 +331,10 @@ def test_rnn_fwd_two_part_matches_gather(gpu, monkeypatch, shape):
     assert np.array_equal(outs[0]["Z"], outs[1]["Z"])
     assert np.array_equal(outs[0]["Y"], outs[1]["Y"])
     Z, Yd = outs[0]["Z"], outs[0]["Y"]
-    eps = 2.0 ** -8
+    # bf16: two roundings of the step's magnitude sum; fp32: the accumulation bound over I+H terms
+    eps = 2.0 ** -8 if dtype == BF16 else 1.01 * (I + H) * 2.0 ** -24
     for t in range(T):
         hprev = h0 if t == 0 else Yd[:, t - 1]
-        zt = X[:, t] @ Wx + hprev @ Wh + b
-        mag = np.abs(X[:, t]) @ np.abs(Wx) + np.abs(hprev) @ np.abs(Wh) + np.abs(b)
+        zt = X[:, t].astype(np.float64) @ Wx + hprev @ Wh + b
+        mag = np.abs(X[:, t]).astype(np.float64) @ np.abs(Wx) + np.abs(hprev) @ np.abs(Wh) + np.abs(b)
         assert np.all(np.abs(Z[:, t] - zt) <= 2 * eps * mag + 1e-6), t
