@@ -7,6 +7,7 @@
 //     these with fp32 atomics; here every sum has a fixed order.)
 #include "gev2_device.hpp"
 #include "gev2_kernels.hpp"
+#include "skinny_nt_impl.hpp"
 
 namespace gev2 {
 
@@ -245,66 +246,20 @@ __global__ void __launch_bounds__(256) finish_col_sums_kernel(const float* parti
 // Skinny NT product for the backward's gA when M <= 16:
 //   D[m][k] = alpha * sum_n G[m][n] * (Z ? act'(Z[m][n]) : 1) * B[k][n].
 // Every output column k is a dot product of one contiguous row of B with the
-// M rows of G, so one wave per k reads that row once in 16-byte chunks (lanes
-// stride over n), keeps M partial sums, and adds them across the wave in a
-// fixed order; G (and Z) are small and come from L2.
+// M rows of G: one wave per k (skinny_nt_column); G (and Z) are small and come
+// from L2.
 template <typename T>
 __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
-  constexpr int EPC = Elem<T>::kPerChunk;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = blockIdx.x * 4 + wave;
   if (k >= p.K) return;                              // wave-uniform; no barrier below
-  const T* G = reinterpret_cast<const T*>(p.G);
-  const T* Z = reinterpret_cast<const T*>(p.Z);
-  const T* brow = reinterpret_cast<const T*>(p.B) + (int64_t)k * p.ldb;
-  float acc[16];
-#pragma unroll
-  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
-  // two passes of 64 chunks at a time, so that both passes' loads are in
-  // flight together; a second pass past N reloads the first and adds nothing
-  for (int n0 = lane * EPC; n0 < p.N; n0 += 128 * EPC) {
-    const int n1 = n0 + 64 * EPC;
-    const bool two = n1 < p.N;
-    const int nb = two ? n1 : n0;
-    u32x4 braw[2], graw[2][16];
-    braw[0] = *reinterpret_cast<const u32x4*>(brow + n0);
-    braw[1] = *reinterpret_cast<const u32x4*>(brow + nb);
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m >= p.M) continue;
-      graw[0][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0);
-      graw[1][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + nb);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (h == 1 && !two) break;
-      const int n = h == 0 ? n0 : nb;
-      float bv[EPC];
-      chunk_to_f32<T>(braw[h], bv);
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        if (m >= p.M) continue;
-        float gv[EPC];
-        chunk_to_f32<T>(graw[h][m], gv);
-        if (Z) {
-          float zv[EPC];
-          chunk_to_f32<T>(*reinterpret_cast<const u32x4*>(Z + (int64_t)m * p.ldz + n), zv);
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) gv[e] *= act_grad(zv[e], p.act, p.slope);
-        }
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[m] = fmaf(gv[e], bv[e], acc[m]);
-      }
-    }
-  }
+  float v[16];
+  skinny_nt_column<T>(p, k, lane, v);
   T* D = reinterpret_cast<T*>(p.D);
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     if (m >= p.M) continue;
-    float v = acc[m];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    if (lane == 0) Elem<T>::store1(D + (int64_t)m * p.ldd + k, p.alpha * v);
+    if (lane == 0) Elem<T>::store1(D + (int64_t)m * p.ldd + k, p.alpha * v[m]);
   }
 }
 

@@ -19,10 +19,11 @@
 // dXH = G' [Wx; Wh]^T, dWcat_t = XH^T G' and dB_t; one kernel adds dWcat_t
 // and dB_t to fp32 sums in step order.  dB is the sum over all steps (the
 // reference's per-step GEMM backward zero-fills it, so it keeps step 0's only).
-// With N <= 16 and N*T <= I+H (rnn_bwd_gathered) the step is shorter: the
-// gather kernel writes G'_t = G * act'(Z_t) into an [N, T, H] buffer and the
-// step runs only dXH = G'_t Wcat^T; dWx = X^T G', dWh = Hprev^T G' and dB are
-// formed once after the loop, each a sum of depth N*T rounded once.
+// With N <= 16 and N*T <= I+H (rnn_bwd_gathered) the step is one kernel:
+// G'_t = G * act'(Z_t) is kept for all steps in an [N, T, H] buffer, step t
+// computes dXH_t = G'_t Wcat^T column by column and turns each column into
+// dX_t or G'_{t-1} at once; dWx = X^T G', dWh = Hprev^T G' and dB are formed
+// once after the loop, each a sum of depth N*T rounded once.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,6 +37,7 @@
 #include "../../include/gev2_gemm.h"
 #include "gev2_device.hpp"
 #include "gev2_kernels.hpp"
+#include "skinny_nt_impl.hpp"
 
 namespace gev2 {
 
@@ -106,6 +108,36 @@ __global__ void __launch_bounds__(256) rnn_bwd_gather_g_kernel(const T* __restri
     const int64_t o = ((int64_t)n * d.T + t) * d.H + h;
     float gy = Elem<T>::load1(dY + o);
     if (!last) gy += Elem<T>::load1(dxh + idx);
+    Elem<T>::store1(gall + o, gy * act_grad(Elem<T>::load1(Z + o), act, slope));
+  }
+}
+
+// Backward step t >= 1 of the gathered-G' form in one kernel: wave k forms
+// column k of dXH_t = G'_t Wcat^T (skinny_nt_column) and consumes it at once,
+// lane m taking row m: a column k < I is dX[m, t, k]; a column I + h is
+// dh_next[m, h], from which the lane forms
+//   G'[m, t-1, h] = (dY[m, t-1, h] + dh_next[m, h]) * act'(Z[m, t-1, h]).
+// dXH itself is never stored.
+template <typename T>
+__global__ void __launch_bounds__(256) rnn_step_nt_kernel(SkinnyNtArgs p, const T* __restrict__ dY,
+                                                          const T* __restrict__ Z, T* __restrict__ gall,
+                                                          T* __restrict__ dX, RnnDims d, int t, int act, float slope) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.x * 4 + wave;
+  if (k >= p.K) return;                              // wave-uniform; no barrier below
+  float v[16];
+  skinny_nt_column<T>(p, k, lane, v);
+  if (lane >= p.M) return;
+  float x = 0.f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m)
+    if (lane == m) x = v[m];
+  const int m = lane;
+  if (k < d.I) {
+    if (dX) Elem<T>::store1(dX + ((int64_t)m * d.T + t) * d.I + k, x);
+  } else {
+    const int64_t o = ((int64_t)m * d.T + t - 1) * d.H + (k - d.I);
+    const float gy = Elem<T>::load1(dY + o) + x;
     Elem<T>::store1(gall + o, gy * act_grad(Elem<T>::load1(Z + o), act, slope));
   }
 }
@@ -246,6 +278,15 @@ hipError_t launch_bwd_gather_g(const void* Z, const void* dY, const void* dxh, v
   hipLaunchKernelGGL((rnn_bwd_gather_g_kernel<T>), dim3(blocks_for((int64_t)d.N * (d.I + d.H))), dim3(256), 0, s,
                      static_cast<const T*>(Z), static_cast<const T*>(dY), static_cast<const T*>(dxh),
                      static_cast<T*>(gall), static_cast<T*>(dX), d, t, act, slope);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_step_nt(const SkinnyNtArgs& a, const void* dY, const void* Z, void* gall, void* dX,
+                          const RnnDims& d, int t, int act, float slope, hipStream_t s) {
+  hipLaunchKernelGGL((rnn_step_nt_kernel<T>), dim3(static_cast<unsigned>((a.K + 3) / 4)), dim3(256), 0, s, a,
+                     static_cast<const T*>(dY), static_cast<const T*>(Z), static_cast<T*>(gall), static_cast<T*>(dX),
+                     d, t, act, slope);
   return hipGetLastError();
 }
 
@@ -618,10 +659,12 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
   const int64_t ldz = (int64_t)d->T * d->H;
   const bool want_w = d->dWx || d->dWh;
   if (rnn_bwd_gathered(d)) {
+    // G'_{T-1} from dY alone; then one kernel per step t >= 1 (dX_t and
+    // G'_{t-1} from dXH_t); step 0's dXH goes to dxh for dX_0 and dh0
+    st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_gather_g, d->Z, d->dY, d->dxh, d->tmpw, d->dX, dm,
+                                      d->T - 1, d->act, d->leaky_slope, s), "gather G'");
+    if (st != GEV2_OK) return st;
     for (int t = d->T - 1; t >= 0; --t) {
-      st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_bwd_gather_g, d->Z, d->dY, d->dxh, d->tmpw, d->dX,
-                                        dm, t, d->act, d->leaky_slope, s), "gather G'");
-      if (st != GEV2_OK) return st;
       gev2::SkinnyNtArgs a{};
       a.G = static_cast<const char*>(d->tmpw) + (size_t)t * d->H * es; a.ldg = ldz;
       a.Z = nullptr; a.ldz = 0;
@@ -629,7 +672,11 @@ int gev2_rnn_bwd(const gev2_rnn_bwd_desc* d, void* stream) {
       a.D = d->dxh; a.ldd = IH;
       a.M = d->N; a.N = d->H; a.K = static_cast<int>(IH);
       a.act = GEV2_ACT_NONE; a.slope = 0.f; a.alpha = 1.f;
-      st = hip_status(gev2::launch_skinny_nt(d->dtype, a, s), "dXH");
+      if (t > 0)
+        st = hip_status(GEV2_RNN_DISPATCH(d->dtype, gev2::launch_step_nt, a, d->dY, d->Z, d->tmpw, d->dX, dm, t,
+                                          d->act, d->leaky_slope, s), "step");
+      else
+        st = hip_status(gev2::launch_skinny_nt(d->dtype, a, s), "dXH");
       if (st != GEV2_OK) return st;
     }
     const int64_t rows = (int64_t)d->N * d->T;
