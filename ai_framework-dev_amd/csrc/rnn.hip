@@ -87,7 +87,8 @@ __global__ void __launch_bounds__(256) rnn_bwd_gather_kernel(const T* __restrict
   }
 }
 
-// Step t of the backward in the gathered-G' form (N <= 16):
+// Step t of the backward in the gathered-G' form (N <= 16; used for the first
+// step, t = T-1, whose G' needs no dh_next):
 //   G'[n, t, :] = (dY[n, t, :] + (t < T-1 ? dxh[n, I:] : 0)) * act'(Z[n, t, :])
 //   dX[n, t+1, :] = dxh[n, :I]            (t < T-1, dX requested)
 // G' ([N, T, H], row stride T*H) is kept for the weight gradients after the loop.
@@ -376,11 +377,11 @@ bool rnn_fwd_two_part(const gev2_rnn_desc* d) {
   return d->ws && (reinterpret_cast<uintptr_t>(d->ws) & 255) == 0 && d->ws_bytes >= need;
 }
 
-// The backward's gathered-G' form: each step forms G'_t straight into an
-// [N, T, H] buffer (tmpw) and runs only dXH = G'_t Wcat^T (skinny NT kernel);
-// after the loop dWx = X^T G' and dWh = Hprev^T G' are one operator forward
-// each (depth N*T, one rounding), Hprev staged in dwcat, and dB is a column
-// sum of G'.  Needs N <= 16, 16-byte rows of G' and wcat, and N*T <= I+H (so
+// The backward's gathered-G' form: G' of every step is kept in an [N, T, H]
+// buffer (tmpw), and a step is one kernel (rnn_step_nt_kernel: dXH_t = G'_t
+// Wcat^T, each column turned at once into dX_t or G'_{t-1}); after the loop
+// dWx = X^T G' and dWh = Hprev^T G' are one operator forward each (depth N*T,
+// one rounding), Hprev staged in dwcat, and dB is a column sum of G'.  Needs N <= 16, 16-byte rows of G' and wcat, and N*T <= I+H (so
 // that G' fits tmpw and Hprev fits dwcat).  GEV2_RNN_STEP_DW=1 keeps the
 // per-step form (one operator backward and one accumulation per step).
 bool rnn_bwd_gathered(const gev2_rnn_bwd_desc* d) {
