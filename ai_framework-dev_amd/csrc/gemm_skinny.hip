@@ -228,10 +228,11 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4& a, const u32x4& b, const 
 
 // W block per workgroup: COLS columns x ROWS rows, 128 KB (COLS 256 or 512);
 // wave w takes COLS / 4 columns over all ROWS rows.
-template <int COLS>
+template <int COLS, int ROWS = 65536 / COLS>
 struct SplitShape {
+  static_assert(ROWS * COLS <= 65536 && ROWS % 128 == 0, "at most 128 KB of W, whole X loads per wave");
   static constexpr int kCols = COLS;
-  static constexpr int kRows = 65536 / COLS;                 // 128 KB of 16-bit W
+  static constexpr int kRows = ROWS;                         // 128 KB of 16-bit W (64 KB at 128 rows)
   static constexpr int kWaveCols = COLS / 4;
   static constexpr int kRowBytes = kWaveCols * 2;            // bytes per W row per wave
   static constexpr int kTiles = kWaveCols / 16;              // 16-column MFMA tiles per wave
@@ -272,10 +273,10 @@ __device__ __forceinline__ int64_t skinny_part_index(int split, int ntile, int t
   return ((int64_t)split * ntile + tile) * (16 * mq) + lane;
 }
 
-template <typename T, int COLS>
+template <typename T, int COLS, int ROWS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_skinny_split_kernel(SkinnyArgs p, f32x4_t* part, int nslab) {
-  using S = SplitShape<COLS>;
+  using S = SplitShape<COLS, ROWS>;
   constexpr int RB = S::kRowBytes;
   constexpr int NWL = S::kLoads;
   constexpr int WBYTES = S::kRows * RB;                      // 32 KB per wave
@@ -436,13 +437,27 @@ __global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArg
     if (m0 + r < p.M) skinny_out_b<T>(p, m0 + r, n, sum[r], bv[r]);
 }
 
-template <typename T, int COLS>
+// K-block rows: the 128 KB block (65536 / cols rows), or 128 rows of a
+// 256-column slab when the 128 KB blocks would give fewer than 128 workgroups
+// (half the CUs), e.g. an RNN step's 8x1536x1024: 24 workgroups of 128 KB
+// become 48 of 64 KB.  K <= 256 stays one K block (its epilogue runs in the
+// kernel, one launch).  GEV2_SKINNY_ROWS=256 keeps the 128 KB block.
+static int skinny_split_rows(int cols, int N, int K) {
+  const int rows = 65536 / cols;
+  if (cols != 256 || K <= 256) return rows;
+  const char* v = std::getenv("GEV2_SKINNY_ROWS");
+  if (v && std::atoi(v) == 256) return rows;
+  const int64_t wgs = (int64_t)((N + cols - 1) / cols) * ((K + rows - 1) / rows);
+  return wgs < 128 ? 128 : rows;
+}
+
+template <typename T, int COLS, int ROWS>
 static hipError_t launch_skinny_split_c(const SkinnyArgs& a, float* part, hipStream_t s) {
-  using S = SplitShape<COLS>;
+  using S = SplitShape<COLS, ROWS>;
   const int nslab = (a.N + S::kCols - 1) / S::kCols;
   const int nsplit = (a.K + S::kRows - 1) / S::kRows;
   f32x4_t* pv = reinterpret_cast<f32x4_t*>(part);
-  hipLaunchKernelGGL((gemm_skinny_split_kernel<T, COLS>), dim3(nslab * nsplit), dim3(256), 0, s, a, pv, nslab);
+  hipLaunchKernelGGL((gemm_skinny_split_kernel<T, COLS, ROWS>), dim3(nslab * nsplit), dim3(256), 0, s, a, pv, nslab);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   const int ntile = nslab * (S::kCols / 16);
@@ -454,13 +469,14 @@ static hipError_t launch_skinny_split_c(const SkinnyArgs& a, float* part, hipStr
 
 template <typename T>
 static hipError_t launch_skinny_split(const SkinnyArgs& a, float* part, hipStream_t s) {
-  return skinny_split_cols() == 512 ? launch_skinny_split_c<T, 512>(a, part, s)
-                                    : launch_skinny_split_c<T, 256>(a, part, s);
+  if (skinny_split_cols() == 512) return launch_skinny_split_c<T, 512, 128>(a, part, s);
+  return skinny_split_rows(256, a.N, a.K) == 128 ? launch_skinny_split_c<T, 256, 128>(a, part, s)
+                                                 : launch_skinny_split_c<T, 256, 256>(a, part, s);
 }
 
 // nsplit x (nslab x tiles per slab) x 16*ceil(M/4) lanes x 16 bytes
 int64_t skinny_split_workspace_bytes(int M, int N, int K) {
-  const int cols = skinny_split_cols(), rows = 65536 / cols;
+  const int cols = skinny_split_cols(), rows = skinny_split_rows(cols, N, K);
   const int64_t nsplit = (K + rows - 1) / rows;
   const int64_t nslab = (N + cols - 1) / cols;
   return nsplit > 1 ? nsplit * nslab * (cols / 16) * 16 * ((M + 3) / 4) * 16 : 0;

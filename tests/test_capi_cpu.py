@@ -117,13 +117,16 @@ def _ws_size(capi, **kw):
 
 
 def test_forward_workspace_size(capi):
-    """Split-K partials of skinny 16-bit problems: K blocks of 256 x 256-column slabs x
-    16 tiles x 16*ceil(M/4) lanes x 16 bytes (= ceil(K/256) * M * N * 4 for M % 4 == 0,
-    N % 256 == 0); none for one K block, fp32 data, the tile path, or empty problems;
-    -1 for a bad descriptor."""
+    """Split-K partials of skinny 16-bit problems: K blocks of 256 rows (128 when 256-row
+    blocks would give fewer than 128 workgroups) x 256-column slabs x 16 tiles x
+    16*ceil(M/4) lanes x 16 bytes (= ceil(K/256) * M * N * 4 for M % 4 == 0, N % 256 == 0);
+    none for one K block, fp32 data, the tile path, or empty problems; -1 for a bad
+    descriptor."""
     assert _ws_size(capi) == 16 * 8 * 4096 * 4
     assert _ws_size(capi, K=4096 + 8) == 17 * 8 * 4096 * 4
-    assert _ws_size(capi, M=5, N=520) == 16 * 3 * 16 * 16 * 2 * 16
+    assert _ws_size(capi, M=5, N=520) == 32 * 3 * 16 * 16 * 2 * 16        # 48 blocks of 256 rows: 128-row blocks
+    assert _ws_size(capi, M=5, N=520, K=512) == 4 * 3 * 16 * 16 * 2 * 16
+    assert _ws_size(capi, M=8, N=1024, K=1536) == 12 * 8 * 1024 * 4         # an RNN step: 12 blocks of 128 rows
     assert _ws_size(capi, K=256) == 0                 # one K block: epilogue in the kernel
     assert _ws_size(capi, dtype=0) == 0               # fp32: dot-product kernel, no workspace
     assert _ws_size(capi, M=64) == 0                  # tile path

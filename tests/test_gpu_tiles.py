@@ -136,6 +136,19 @@ def test_skinny_variants_exact(gpu, monkeypatch, variant, shape, dtype):
     assert np.array_equal(Y, Yr), f"Y {shape}"
 
 
+@pytest.mark.parametrize("shape", [(13, 264, 328), (5, 136, 2056), (8, 1024, 1536)], ids=lambda s: "x".join(map(str, s)))
+def test_skinny_256_row_blocks_exact(gpu, monkeypatch, shape):
+    """GEV2_SKINNY_ROWS=256 keeps 256-row K blocks where the default takes 128-row ones (fewer
+    than 128 workgroups of 256 rows): both exact on integer inputs."""
+    capi = gpu
+    monkeypatch.setenv("GEV2_SKINNY_ROWS", "256")
+    M, N, K = shape
+    Y, Z, Yr, Zr, path = _run(capi, "NN", M, N, K, 0, BF16, O.BIAS_PERN, "relu", seed=M + K)
+    assert path == "skinny:split", path
+    assert np.array_equal(Z, Zr), f"Z {shape}"
+    assert np.array_equal(Y, Yr), f"Y {shape}"
+
+
 def test_skinny_explicit_workspace(gpu):
     """A caller-provided workspace (gev2_gemm_fwd_workspace_size bytes) gives the same
     bits as the library's per-stream buffer, and two problems in a row that share it
@@ -155,9 +168,13 @@ def test_skinny_explicit_workspace(gpu):
                           act="relu")
                 need = capi.fwd_workspace_size(**kw)
                 # K blocks x column slabs x (cols / 16) tiles x 16*ceil(M/4) lanes x 16 bytes, for
-                # 256-column x 256-row W blocks (GEV2_SKINNY_COLS=512: 512 x 128)
+                # 256-column x 256-row W blocks (GEV2_SKINNY_COLS=512: 512 x 128; 256 x 128 when
+                # 256-row blocks would give fewer than 128 workgroups and K > 256)
                 cols = 512 if os.environ.get("GEV2_SKINNY_COLS") == "512" else 256
                 rows = 65536 // cols
+                if cols == 256 and K > 256 and -(-N // 256) * -(-K // 256) < 128 and \
+                        os.environ.get("GEV2_SKINNY_ROWS") != "256":
+                    rows = 128
                 assert need == -(-K // rows) * -(-N // cols) * (cols // 16) * 16 * -(-M // 4) * 16
                 if own:
                     kw.update(workspace=dev.empty(need), workspace_bytes=need)
