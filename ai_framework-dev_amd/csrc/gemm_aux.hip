@@ -248,13 +248,13 @@ __global__ void __launch_bounds__(256) finish_col_sums_kernel(const float* parti
 // Every output column k is a dot product of one contiguous row of B with the
 // M rows of G: one wave per k (skinny_nt_column); G (and Z) are small and come
 // from L2.
-template <typename T>
+template <typename T, int MAXM>
 __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = blockIdx.x * 4 + wave;
   if (k >= p.K) return;                              // wave-uniform; no barrier below
   float v[16];
-  skinny_nt_column<T>(p, k, lane, v);
+  skinny_nt_column<T, MAXM, skinny_nt_passes<T>(MAXM)>(p, k, lane, v);
   T* D = reinterpret_cast<T*>(p.D);
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
@@ -266,9 +266,18 @@ __global__ void __launch_bounds__(256) skinny_nt_kernel(SkinnyNtArgs p) {
 hipError_t launch_skinny_nt(int dtype, const SkinnyNtArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.K + 3) / 4));
   switch (dtype) {
-    case kF32: hipLaunchKernelGGL(skinny_nt_kernel<float>, grid, dim3(256), 0, s, a); break;
-    case kBF16: hipLaunchKernelGGL(skinny_nt_kernel<__bf16>, grid, dim3(256), 0, s, a); break;
-    case kF16: hipLaunchKernelGGL(skinny_nt_kernel<_Float16>, grid, dim3(256), 0, s, a); break;
+    case kF32:
+      if (a.M <= 8) hipLaunchKernelGGL((skinny_nt_kernel<float, 8>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((skinny_nt_kernel<float, 16>), grid, dim3(256), 0, s, a);
+      break;
+    case kBF16:
+      if (a.M <= 8) hipLaunchKernelGGL((skinny_nt_kernel<__bf16, 8>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((skinny_nt_kernel<__bf16, 16>), grid, dim3(256), 0, s, a);
+      break;
+    case kF16:
+      if (a.M <= 8) hipLaunchKernelGGL((skinny_nt_kernel<_Float16, 8>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((skinny_nt_kernel<_Float16, 16>), grid, dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

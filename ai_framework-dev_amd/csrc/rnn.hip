@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(256) rnn_bwd_gather_g_kernel(const T* __restri
 // dh_next[m, h], from which the lane forms
 //   G'[m, t-1, h] = (dY[m, t-1, h] + dh_next[m, h]) * act'(Z[m, t-1, h]).
 // dXH itself is never stored.
-template <typename T>
+template <typename T, int MAXM>
 __global__ void __launch_bounds__(256) rnn_step_nt_kernel(SkinnyNtArgs p, const T* __restrict__ dY,
                                                           const T* __restrict__ Z, T* __restrict__ gall,
                                                           T* __restrict__ dX, RnnDims d, int t, int act, float slope) {
@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(256) rnn_step_nt_kernel(SkinnyNtArgs p, const 
   const int k = blockIdx.x * 4 + wave;
   if (k >= p.K) return;                              // wave-uniform; no barrier below
   float v[16];
-  skinny_nt_column<T>(p, k, lane, v);
+  skinny_nt_column<T, MAXM, skinny_nt_passes<T>(MAXM)>(p, k, lane, v);
   if (lane >= p.M) return;
   float x = 0.f;
 #pragma unroll
@@ -285,9 +285,13 @@ hipError_t launch_bwd_gather_g(const void* Z, const void* dY, const void* dxh, v
 template <typename T>
 hipError_t launch_step_nt(const SkinnyNtArgs& a, const void* dY, const void* Z, void* gall, void* dX,
                           const RnnDims& d, int t, int act, float slope, hipStream_t s) {
-  hipLaunchKernelGGL((rnn_step_nt_kernel<T>), dim3(static_cast<unsigned>((a.K + 3) / 4)), dim3(256), 0, s, a,
-                     static_cast<const T*>(dY), static_cast<const T*>(Z), static_cast<T*>(gall), static_cast<T*>(dX),
-                     d, t, act, slope);
+  const dim3 grid(static_cast<unsigned>((a.K + 3) / 4));
+  if (a.M <= 8)
+    hipLaunchKernelGGL((rnn_step_nt_kernel<T, 8>), grid, dim3(256), 0, s, a, static_cast<const T*>(dY),
+                       static_cast<const T*>(Z), static_cast<T*>(gall), static_cast<T*>(dX), d, t, act, slope);
+  else
+    hipLaunchKernelGGL((rnn_step_nt_kernel<T, 16>), grid, dim3(256), 0, s, a, static_cast<const T*>(dY),
+                       static_cast<const T*>(Z), static_cast<T*>(gall), static_cast<T*>(dX), d, t, act, slope);
   return hipGetLastError();
 }
 

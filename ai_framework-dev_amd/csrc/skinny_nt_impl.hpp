@@ -12,38 +12,44 @@
 
 namespace gev2 {
 
-template <typename T>
+template <typename T, int MAXM = 16, int P = 2>
 __device__ __forceinline__ void skinny_nt_column(const SkinnyNtArgs& p, int k, int lane, float* sum) {
   constexpr int EPC = Elem<T>::kPerChunk;
   const T* G = reinterpret_cast<const T*>(p.G);
   const T* Z = reinterpret_cast<const T*>(p.Z);
   const T* brow = reinterpret_cast<const T*>(p.B) + (int64_t)k * p.ldb;
-  float acc[16];
+  float acc[MAXM];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
-  // two passes of 64 chunks at a time, so that both passes' loads are in
-  // flight together; a second pass past N reloads the first and adds nothing
-  for (int n0 = lane * EPC; n0 < p.N; n0 += 128 * EPC) {
-    const int n1 = n0 + 64 * EPC;
-    const bool two = n1 < p.N;
-    const int nb = two ? n1 : n0;
-    u32x4 braw[2], graw[2][16];
-    braw[0] = *reinterpret_cast<const u32x4*>(brow + n0);
-    braw[1] = *reinterpret_cast<const u32x4*>(brow + nb);
+  for (int m = 0; m < MAXM; ++m) acc[m] = 0.f;
+  // P passes of 64 chunks at a time, so that all their loads are in flight
+  // together; a pass past N reloads the first and adds nothing.  A lane adds
+  // its chunks in increasing n whatever P is.
+  for (int n0 = lane * EPC; n0 < p.N; n0 += P * 64 * EPC) {
+    int nn[P];
+    bool ok[P];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
+    for (int h = 0; h < P; ++h) {
+      const int nh = n0 + h * 64 * EPC;
+      ok[h] = nh < p.N;
+      nn[h] = ok[h] ? nh : n0;
+    }
+    u32x4 braw[P], graw[P][MAXM];
+#pragma unroll
+    for (int h = 0; h < P; ++h) braw[h] = *reinterpret_cast<const u32x4*>(brow + nn[h]);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
       if (m >= p.M) continue;
-      graw[0][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + n0);
-      graw[1][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + nb);
+#pragma unroll
+      for (int h = 0; h < P; ++h) graw[h][m] = *reinterpret_cast<const u32x4*>(G + (int64_t)m * p.ldg + nn[h]);
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (h == 1 && !two) break;
-      const int n = h == 0 ? n0 : nb;
+    for (int h = 0; h < P; ++h) {
+      if (!ok[h]) break;
+      const int n = nn[h];
       float bv[EPC];
       chunk_to_f32<T>(braw[h], bv);
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
+      for (int m = 0; m < MAXM; ++m) {
         if (m >= p.M) continue;
         float gv[EPC];
         chunk_to_f32<T>(graw[h][m], gv);
@@ -59,7 +65,7 @@ __device__ __forceinline__ void skinny_nt_column(const SkinnyNtArgs& p, int k, i
     }
   }
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
+  for (int m = 0; m < MAXM; ++m) {
     if (m >= p.M) continue;
     float v = acc[m];
 #pragma unroll
@@ -67,5 +73,10 @@ __device__ __forceinline__ void skinny_nt_column(const SkinnyNtArgs& p, int k, i
     sum[m] = v;
   }
 }
+
+// Rows and passes for a problem: up to 8 rows keep four passes of fp32
+// chunks in flight (graw: 4 x 8 chunks), 16 rows two.
+template <typename T>
+constexpr int skinny_nt_passes(int maxm) { return (maxm == 8 && sizeof(T) == 4) ? 4 : 2; }
 
 }  // namespace gev2
