@@ -441,12 +441,14 @@ __global__ void __launch_bounds__(kReduceThreads) skinny_reduce_kernel(SkinnyArg
 // 256-column slab when the 128 KB blocks would give fewer than 128 workgroups
 // (half the CUs), e.g. an RNN step's 8x1536x1024: 24 workgroups of 128 KB
 // become 48 of 64 KB.  K <= 256 stays one K block (its epilogue runs in the
-// kernel, one launch).  GEV2_SKINNY_ROWS=256 keeps the 128 KB block.
+// kernel, one launch).  GEV2_SKINNY_ROWS=256 / 128 picks one of the two
+// (tuning runs).
 static int skinny_split_rows(int cols, int N, int K) {
   const int rows = 65536 / cols;
   if (cols != 256 || K <= 256) return rows;
   const char* v = std::getenv("GEV2_SKINNY_ROWS");
   if (v && std::atoi(v) == 256) return rows;
+  if (v && std::atoi(v) == 128) return 128;
   const int64_t wgs = (int64_t)((N + cols - 1) / cols) * ((K + rows - 1) / rows);
   return wgs < 128 ? 128 : rows;
 }
