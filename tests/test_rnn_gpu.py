@@ -126,13 +126,16 @@ def test_rnn_exact_integers_both_backward_forms(env, monkeypatch, form):
         assert np.array_equal(out[k], ref[k]), k
 
 
+@pytest.mark.parametrize("shape", [(8, 4, 512, 1024), (13, 3, 256, 264)], ids=["N8-H1024", "N13-H264"])
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
-def test_rnn_backward_forms_agree(env, monkeypatch, dtype):
+def test_rnn_backward_forms_agree(env, monkeypatch, dtype, shape):
     """The gathered-G' backward against the per-step one on the benchmark's shape class
-    (N 8, I 512, H 1024, fewer steps): dh0 and dX are the same chain of dXH products (equal
-    up to the per-step form's rounding of G before act'), dWx / dWh / dB differ only in
-    summation order and rounding (one rounding of a depth-N*T sum against T roundings)."""
-    N, T, I, H = 8, 4, 512, 1024
+    (N 8, I 512, H 1024, fewer steps; the step kernel for at most 8 rows) and on 13 rows with
+    H = 264 (the 16-row step kernel, a ragged last pass of each dXH column): dh0 and dX are the
+    same chain of dXH products (equal up to the per-step form's rounding of G before act'),
+    dWx / dWh / dB differ only in summation order and rounding (one rounding of a depth-N*T
+    sum against T roundings)."""
+    N, T, I, H = shape
     X, Wx, Wh, h0, b, dY = _inputs(19, N, T, I, H)
     if dtype == BF16:
         X, Wx, Wh, h0, dY = (rounded(a, BF16).astype(np.float32) for a in (X, Wx, Wh, h0, dY))
